@@ -1,0 +1,276 @@
+"""Benchmark of the GL-SDM memory operator on one MI355X (headline config).
+
+Workload: B=8 requests, T=2048 tokens in 4 commit
+epochs of C=512, H=8 heads, bank M=65536 slots per head (half=256, L=512
+factor scores per head), key dim dk=128, value dim D=128 (H*D = 1024), top-k
+16, bf16 bank/queries/deltas, fp32 accumulation.  One step = all 4 epochs of:
+
+  score(read queries) -> route -> snapshot read          (read path)
+  score(write queries) -> route -> proposal keys -> commit (write path)
+
+with the bank updated in place at every 512-token clock (donated commit).
+Inputs are synthetic, generated on the CPU with a seeded generator and copied
+to HBM before the timed region.  Prints one JSON line (see the driver
+contract); rank 0 only, one GPU.
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gl-sdm_amd"))
+
+HBM_PEAK = 8.0e12          # B/s, MI355X
+MFMA_BF16_PEAK = 2.5e15    # FLOP/s dense bf16
+
+CFG = dict(B=8, T=2048, C=512, H=8, half=256, dk=128, D=128, k=16)
+
+
+def make_inputs(cfg, seed=0):
+    """Seeded CPU generation in a fixed order, then bf16 (config-2 protocol)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    B, T, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "H", "half", "dk", "D", "k"))
+    norm = torch.nn.functional.normalize
+    keys = norm(torch.randn(H, 2 * half, dk, generator=g), dim=-1).bfloat16()
+    bank = (torch.randn(H, half * half, D, generator=g) * 0.02).bfloat16()
+    qr = norm(torch.randn(B, T, H, dk, generator=g), dim=-1).bfloat16()
+    qw = norm(torch.randn(B, T, H, dk, generator=g), dim=-1).bfloat16()
+    delta = (torch.randn(B, T, H, k, D, generator=g) * 0.02).bfloat16()
+    return keys, bank, qr, qw, delta
+
+
+class Pipeline:
+    """Preallocated buffers and direct C-ABI calls for one epoch of the op."""
+
+    def __init__(self, cfg, device):
+        from glsdm import _native as N
+        self.N, self.cfg, self.dev = N, cfg, device
+        keys, bank, qr, qw, delta = make_inputs(cfg)
+        B, T, C, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "C", "H", "half", "dk", "D", "k"))
+        self.epochs = T // C
+        self.keys = keys.to(device)
+        self.bank = bank.unsqueeze(0).expand(B, -1, -1, -1).contiguous().to(device)   # per-request replicas
+        split = lambda x: [x[:, e * C:(e + 1) * C].contiguous().to(device) for e in range(self.epochs)]
+        self.qr, self.qw, self.delta = split(qr), split(qw), split(delta)
+        L = 2 * half
+        self.scores = torch.empty(B, C, H, L, dtype=torch.float32, device=device)
+        self.idx = torch.empty(B, C, H, k, dtype=torch.int64, device=device)
+        self.w = torch.empty(B, C, H, k, dtype=torch.float32, device=device)
+        self.out = torch.empty(B, C, H, D, dtype=torch.float32, device=device)
+        self.widx = torch.empty_like(self.idx)
+        self.ww = torch.empty_like(self.w)
+        self.addr = torch.empty_like(self.idx)
+        self.ckeys = torch.empty_like(self.idx)
+        self.rows = B * H * half * half
+        self.E = B * C * H * k
+        self.key_bits = (self.rows * C - 1).bit_length()
+        size = ctypes.c_size_t(0)
+        N.call("glsdm_commit_workspace_bytes", self.E, self.key_bits, ctypes.byref(size))
+        self.ws = torch.empty(size.value, dtype=torch.uint8, device=device)
+        self.unique = torch.zeros(1, dtype=torch.int64, device=device)
+        self.stream = N.stream(device)
+        self.timers = None
+
+    def _timed(self, name, fn):
+        if self.timers is None:
+            return fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        self.timers.setdefault(name, []).append((a, b))
+
+    def epoch(self, e, count_unique=False):
+        N, c, p, st = self.N, self.cfg, self.N.ptr, self.stream
+        B, C, H, half, dk, D, k = (c[x] for x in ("B", "C", "H", "half", "dk", "D", "k"))
+        S = half * half
+        self._timed("score", lambda: N.call("glsdm_score", p(self.qr[e]), p(self.keys), B, C, H, dk, half,
+                                            p(self.scores), st))
+        self._timed("route", lambda: N.call("glsdm_route", p(self.scores), B * C * H, half, k, N.TIE_HIGHEST,
+                                            p(self.idx), p(self.w), st))
+        self._timed("read", lambda: N.call("glsdm_read", p(self.bank), N.BF16, B, H, S, D, C, k, p(self.idx),
+                                           p(self.w), p(self.out), N.F32, st))
+        self._timed("score", lambda: N.call("glsdm_score", p(self.qw[e]), p(self.keys), B, C, H, dk, half,
+                                            p(self.scores), st))
+        self._timed("route", lambda: N.call("glsdm_route", p(self.scores), B * C * H, half, k, N.TIE_HIGHEST,
+                                            p(self.widx), p(self.ww), st))
+        self._timed("keys", lambda: N.call("glsdm_proposal_keys", p(self.widx), B, C, H, k, S, 0, C, 1, 0,
+                                           p(self.addr), p(self.ckeys), st))
+        self._timed("commit", lambda: N.call("glsdm_commit", p(self.bank), N.BF16, self.rows, D, p(self.addr),
+                                             p(self.delta[e]), N.BF16, p(self.ckeys), 0, self.key_bits, self.E,
+                                             p(self.ws), self.ws.numel(),
+                                             p(self.unique) if count_unique else None, st))
+
+    def step(self):
+        for e in range(self.epochs):
+            self.epoch(e)
+
+    def unique_rows(self):
+        """Touched rows U per epoch (untimed pass on a scratch copy of the bank)."""
+        saved = self.bank
+        self.bank = saved.clone()
+        out = []
+        for e in range(self.epochs):
+            self.unique.zero_()
+            self.epoch(e, count_unique=True)
+            torch.cuda.synchronize()
+            out.append(int(self.unique.item()))
+        self.bank = saved
+        return out
+
+
+def algorithmic_bytes(cfg, unique):
+    """Read + commit HBM bytes per epoch (bf16 bank/queries/deltas)."""
+    B, C, H, dk, D, k = (cfg[x] for x in ("B", "C", "H", "dk", "D", "k"))
+    rows = B * C * H
+    read_kernel = rows * (k * D * 2 + D * 4 + k * 12)            # gathers + fp32 out + idx/w
+    read = read_kernel + rows * dk * 2                            # + queries read once
+    E = rows * k
+    commit = [E * D * 2 + E * 16 + 2 * u * D * 2 for u in unique]
+    return read, read_kernel, commit
+
+
+def cpu_baseline(cfg, budget_s=12.0):
+    """Scalar C oracle (oracle/glsdm_oracle.c, 1 thread) on a bounded sample of the
+    same workload: whole epochs for request 0, repeated until ~budget_s."""
+    from oracle import c_oracle
+    keys, bank, qr, qw, delta = make_inputs(cfg)
+    C, H, half, D, k = (cfg[x] for x in ("C", "H", "half", "D", "k"))
+    S = half * half
+    bank0 = bank.float().reshape(1, H, S, D)
+    flat = bank0.reshape(-1, D).clone()
+    tokens, t0, e = 0, time.perf_counter(), 0
+    while True:
+        sl = slice(e * C, (e + 1) * C)
+        sr = c_oracle.score(qr[:1, sl], keys)
+        idx, w = c_oracle.route(sr, k)
+        c_oracle.read(flat.view(1, H, S, D), idx, w)
+        sw = c_oracle.score(qw[:1, sl], keys)
+        widx, _ = c_oracle.route(sw, k)
+        addr = (torch.arange(H).view(1, 1, H, 1) * S + widx).reshape(-1)
+        ck = addr * C + torch.arange(C).view(1, C, 1, 1).expand(1, C, H, k).reshape(-1)
+        lib = c_oracle.lib()
+        d = delta[:1, sl].float().reshape(-1, D).contiguous()
+        lib.oracle_commit(flat.data_ptr(), flat.shape[0], D, addr.data_ptr(), d.data_ptr(), ck.data_ptr(),
+                          addr.numel())
+        tokens += C
+        e = (e + 1) % (cfg["T"] // C)
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": tokens / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"request 0 of config 2, {tokens} tokens ({tokens // C} epochs of 512): "
+                      f"scoring + route + read + route + commit, fp32 scalar C oracle, {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the operator shards by request/head with no exchange; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    cfg = CFG
+    pipe = Pipeline(cfg, dev)
+    unique = pipe.unique_rows()
+    for _ in range(args.warmup):
+        pipe.step()
+    torch.cuda.synchronize()
+
+    pipe.timers = {}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        pipe.step()
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_step = total_ms / args.steps
+    per_call = {n: statistics.mean(a.elapsed_time(b) for a, b in v) for n, v in pipe.timers.items()}
+    calls = {n: len(v) // args.steps for n, v in pipe.timers.items()}
+
+    tokens = cfg["B"] * cfg["T"]
+    read_b, read_kernel_b, commit_b = algorithmic_bytes(cfg, unique)
+    epochs = pipe.epochs
+    alg_total = epochs * read_b + sum(commit_b)
+    # dominant call: largest share of step time
+    share = {n: per_call[n] * calls[n] for n in per_call}
+    dominant = max(share, key=share.get)
+    if dominant == "read":
+        bytes_launch, t_launch = read_kernel_b, per_call["read"] * 1e-3
+        roof = {"kernel": "read_kernel (glsdm_read)", "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK / 1e9}
+        achieved = bytes_launch / t_launch / 1e9
+    elif dominant == "commit":
+        bytes_launch, t_launch = statistics.mean(commit_b), per_call["commit"] * 1e-3
+        roof = {"kernel": "glsdm_commit (pack + radix passes + segment)", "bound": "hbm", "unit": "GB/s",
+                "peak": HBM_PEAK / 1e9}
+        achieved = bytes_launch / t_launch / 1e9
+    elif dominant == "route":
+        # selection is VALU work on fp32 scores read from HBM
+        bytes_launch = cfg["B"] * cfg["C"] * cfg["H"] * (2 * cfg["half"] * 4 + cfg["k"] * 12)
+        t_launch = per_call["route"] * 1e-3
+        roof = {"kernel": "route_kernel (glsdm_route)", "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK / 1e9}
+        achieved = bytes_launch / t_launch / 1e9
+    else:
+        flops = 2 * cfg["B"] * cfg["C"] * cfg["H"] * 2 * cfg["half"] * cfg["dk"]
+        t_launch = per_call["score"] * 1e-3
+        roof = {"kernel": "score_kernel (glsdm_score)", "bound": "mfma", "unit": "TFLOP/s",
+                "peak": MFMA_BF16_PEAK / 1e12}
+        achieved = flops / t_launch / 1e12
+        bytes_launch = None
+    roof.update({"achieved": round(achieved, 1), "frac": round(achieved / roof["peak"], 4), "traffic": None})
+
+    scoring_flops = 2 * cfg["B"] * cfg["C"] * cfg["H"] * 2 * cfg["half"] * cfg["dk"]
+    rc_time = epochs * (per_call["read"] + per_call["commit"]) * 1e-3
+    result = {
+        "metric": "GL-SDM mem-op tokens/s + % HBM roofline (read+commit); full-stack tokens/s",
+        "value": round(tokens / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded CPU generator, config-2 protocol)",
+        "config": {"workload": "memory op, BASELINE configs[1]: B=8 T=2048 (4 epochs of 512) H=8 M=65536 "
+                               "dk=128 D=128 k=16 bf16, score+route+read+route+commit",
+                   "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
+                   "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "read_commit_hbm": {"bytes_per_step": alg_total, "seconds_per_step": rc_time,
+                            "achieved_GBps": round(alg_total / rc_time / 1e9, 1),
+                            "frac": round(alg_total / rc_time / HBM_PEAK, 4),
+                            "op_frac": round(alg_total / (ms_step * 1e-3) / HBM_PEAK, 4)},
+        "scoring_mfma": {"flops_per_call": scoring_flops, "ms_per_call": round(per_call["score"], 5),
+                         "frac": round(scoring_flops / (per_call["score"] * 1e-3) / MFMA_BF16_PEAK, 4)},
+        "ms_per_call": {n: round(v, 5) for n, v in per_call.items()},
+        "calls_per_step": calls,
+        "unique_rows_per_epoch": unique,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

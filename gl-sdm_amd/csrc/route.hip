@@ -1,0 +1,217 @@
+// Product-key routing of fp32 factor scores on gfx950.
+//
+// Semantics (S/ = projects/gl-sdm/src/gl_sdm/): S/memory/routing.py:10-26 with
+// tie HIGHEST, S/layers/router.py:39-61 with tie LOWEST.  Every element is
+// ranked by a distinct 64-bit key (monotone score bits << 32 | tie bits of its
+// index), which is the total order the reference's chain of stable argsorts
+// induces, so "top-k by key" reproduces the reference's selection exactly,
+// including ties and signed zeros.
+//
+// Work decomposition: a group of G adjacent lanes owns one score row.  Each
+// lane keeps a descending top-K list of 64-bit keys in registers (K = width
+// rounded up to a power of two).  It streams its strided share of the row in
+// chunks of K: a chunk is sorted by a bitonic network and merged into the list
+// by a bitonic merge that keeps the K largest.  The G lists of the group are
+// then merged by a butterfly over __shfl_xor, after which every lane of the
+// group holds the row's exact top-K.  Factor lists go through LDS to the
+// candidate stage (kk*kk fp32 sums), which runs the same selection; the chosen
+// slots are sorted ascending and weighted by a softmax.
+#include "glsdm_internal.h"
+
+namespace glsdm {
+
+template <int K, bool DESC>
+__device__ __forceinline__ void bitonic_sort(uint64_t (&v)[K])
+{
+#pragma unroll
+    for (int size = 2; size <= K; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+            for (int i = 0; i < K; ++i) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool down = ((i & size) == 0) == DESC;
+                    const uint64_t a = v[i], b = v[j];
+                    const bool swap = down ? (a < b) : (a > b);
+                    v[i] = swap ? b : a;
+                    v[j] = swap ? a : b;
+                }
+            }
+        }
+    }
+}
+
+// t <- the K largest of t U c; both sorted descending, result sorted descending.
+template <int K>
+__device__ __forceinline__ void merge_top(uint64_t (&t)[K], const uint64_t (&c)[K])
+{
+#pragma unroll
+    for (int i = 0; i < K; ++i) t[i] = t[i] > c[K - 1 - i] ? t[i] : c[K - 1 - i];
+#pragma unroll
+    for (int stride = K >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            const int j = i ^ stride;
+            if (j > i) {
+                const uint64_t a = t[i], b = t[j];
+                t[i] = a > b ? a : b;
+                t[j] = a > b ? b : a;
+            }
+        }
+    }
+}
+
+// Exact top-K keys of `n` elements produced by key_of(i), for the G-lane group
+// that lane g belongs to.  All lanes of the group return the same sorted list.
+template <int K, int G, typename KeyOf>
+__device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (&t)[K])
+{
+#pragma unroll
+    for (int i = 0; i < K; ++i) t[i] = 0;
+    for (int base = 0; base < n; base += G * K) {
+        uint64_t c[K];
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            const int i = base + q * G + g;
+            c[q] = i < n ? key_of(i) : 0;
+        }
+        bitonic_sort<K, true>(c);
+        merge_top<K>(t, c);
+    }
+#pragma unroll
+    for (int s = 1; s < G; s <<= 1) {
+        uint64_t p[K];
+#pragma unroll
+        for (int q = 0; q < K; ++q) p[q] = shfl_xor_u64(t[q], s);
+        merge_top<K>(t, p);
+    }
+}
+
+template <int K, int G>
+__global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ scores, int64_t rows,
+                                                    int half, int width, int tie,
+                                                    int64_t *__restrict__ index,
+                                                    float *__restrict__ weights)
+{
+    constexpr int RPB = 256 / G;
+    __shared__ uint32_t s_idx[RPB][2][K];
+    __shared__ float s_val[RPB][2][K];
+
+    const int lr = threadIdx.x / G;
+    const int g = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;
+    const float *src = scores + r * 2 * (int64_t)half;
+    const int kk = width < half ? width : half;
+
+    // 1. per-factor top-kk sub-keys (stashed in LDS for the candidate grid)
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        const float *fs = src + f * half;
+        uint64_t t[K];
+        group_top<K, G>(half, g, [&](int i) { return rank_key(fs[i], (uint32_t)i, tie); }, t);
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if (i % G == g && i < kk) {
+                const uint32_t id = rank_index(t[i], tie);
+                s_idx[lr][f][i] = id;
+                s_val[lr][f][i] = fs[id];
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. best `width` cells of the kk x kk grid of fp32 sums
+    const uint32_t *i0 = s_idx[lr][0], *i1 = s_idx[lr][1];
+    const float *v0 = s_val[lr][0], *v1 = s_val[lr][1];
+    uint64_t t[K];
+    group_top<K, G>(kk * kk, g, [&](int c) {
+        const int i = c / kk, j = c - i * kk;
+        const float s = v0[i] + v1[j];
+        return rank_key(s, i0[i] * (uint32_t)half + i1[j], tie);
+    }, t);
+
+    // 3. chosen slots in ascending order, softmax over their sums
+    uint64_t u[K];
+#pragma unroll
+    for (int w = 0; w < K; ++w) {
+        if (w < width) {
+            const uint32_t slot = rank_index(t[w], tie);
+            const float s = order_value((uint32_t)(t[w] >> 32));
+            u[w] = ((uint64_t)slot << 32) | __float_as_uint(s);
+        } else {
+            u[w] = ~0ull;
+        }
+    }
+    bitonic_sort<K, false>(u);
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < K; ++w) {
+        if (w < width) {
+            const float s = __uint_as_float((uint32_t)u[w]);
+            m = (s > m || s != s) ? s : m;
+        }
+    }
+    float e[K];
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < K; ++w) {
+        if (w < width) {
+            e[w] = expf(__uint_as_float((uint32_t)u[w]) - m);
+            total += e[w];
+        }
+    }
+    const float inv = 1.0f / total;
+    if (live) {
+#pragma unroll
+        for (int w = 0; w < K; ++w) {
+            if (w < width && w % G == g) {
+                index[row * width + w] = (int64_t)(u[w] >> 32);
+                weights[row * width + w] = e[w] * inv;
+            }
+        }
+    }
+}
+
+template <int K, int G>
+static int launch_route(const float *scores, int64_t rows, int half, int width, int tie,
+                        int64_t *index, float *weights, hipStream_t st)
+{
+    constexpr int RPB = 256 / G;
+    const int64_t blocks = ceil_div(rows, RPB);
+    hipLaunchKernelGGL((route_kernel<K, G>), dim3((unsigned)blocks), dim3(256), 0, st, scores, rows,
+                       half, width, tie, index, weights);
+    return check_launch("route_kernel");
+}
+
+int route_launch(const float *scores, int64_t rows, int half, int width, int tie, int64_t *index,
+                 float *weights, hipStream_t st)
+{
+    if (rows < 0) return fail(GLSDM_ERR_ARG, "route: rows must be >= 0");
+    if (half < 1 || half > 65535) return fail(GLSDM_ERR_UNSUPPORTED, "route: half must be in [1, 65535]");
+    if (width < 1 || width > 64) return fail(GLSDM_ERR_UNSUPPORTED, "route: width must be in [1, 64]");
+    if ((int64_t)width > (int64_t)half * half) return fail(GLSDM_ERR_ARG, "route: width exceeds slots");
+    if (tie != GLSDM_TIE_HIGHEST && tie != GLSDM_TIE_LOWEST) return fail(GLSDM_ERR_ARG, "route: bad tie rule");
+    if (rows == 0) return GLSDM_OK;
+    if (!scores || !index || !weights) return fail(GLSDM_ERR_ARG, "route: null pointer");
+    if (rows > (int64_t)0x7FFFFFFF * 8) return fail(GLSDM_ERR_UNSUPPORTED, "route: too many rows");
+    switch (pow2_ceil(width)) {
+    case 1: return launch_route<1, 4>(scores, rows, half, width, tie, index, weights, st);
+    case 2: return launch_route<2, 4>(scores, rows, half, width, tie, index, weights, st);
+    case 4: return launch_route<4, 4>(scores, rows, half, width, tie, index, weights, st);
+    case 8: return launch_route<8, 4>(scores, rows, half, width, tie, index, weights, st);
+    case 16: return launch_route<16, 4>(scores, rows, half, width, tie, index, weights, st);
+    case 32: return launch_route<32, 8>(scores, rows, half, width, tie, index, weights, st);
+    default: return launch_route<64, 8>(scores, rows, half, width, tie, index, weights, st);
+    }
+}
+
+}  // namespace glsdm
+
+extern "C" int glsdm_route(const float *scores, int64_t rows, int32_t half, int32_t width, int32_t tie,
+                           int64_t *index, float *weights, void *stream)
+{
+    return glsdm::route_launch(scores, rows, half, width, tie, index, weights, glsdm::as_stream(stream));
+}

@@ -1,0 +1,103 @@
+"""ctypes binding of libglsdm.so (declared in include/glsdm.h).
+
+The library is the only compute path of this package: if it is missing, or no
+HIP device is present, every native call raises instead of falling back.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libglsdm.so")
+
+F32, BF16 = 0, 1
+TIE_HIGHEST, TIE_LOWEST = 0, 1
+TIES = {"highest": TIE_HIGHEST, "lowest": TIE_LOWEST}
+DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
+
+OK, ERR_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_HIP = 0, -1, -2, -3, -4
+
+_P, _I64, _I32, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t
+SIGNATURES = {
+    "glsdm_version": ([], ctypes.c_char_p),
+    "glsdm_last_error": ([], ctypes.c_char_p),
+    "glsdm_route": ([_P, _I64, _I32, _I32, _I32, _P, _P, _P], _I32),
+    "glsdm_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _I32, _P], _I32),
+    "glsdm_route_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _P, _I32, _P, _P, _P], _I32),
+    "glsdm_score": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P], _I32),
+    "glsdm_commit_workspace_bytes": ([_I64, _I32, ctypes.POINTER(_SZ)], _I32),
+    "glsdm_commit": ([_P, _I32, _I64, _I64, _P, _P, _I32, _P, _I64, _I32, _I64, _P, _SZ, _P, _P], _I32),
+    "glsdm_absolute_addresses": ([_P, _I64, _I64, _I64, _I32, _I64, _P, _P], _I32),
+    "glsdm_proposal_keys": ([_P, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),
+    "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libglsdm.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NativeError(f"{LIB_PATH} is missing: build it with `python gl-sdm_amd/build.py` "
+                                      "(or __graft_entry__.build()); there is no fallback path")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (args, res) in SIGNATURES.items():
+                    fn = getattr(L, name)
+                    fn.argtypes, fn.restype = args, res
+                _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Invoke an entry point and turn a non-zero status into an exception."""
+    rc = getattr(lib(), name)(*args)
+    if rc != OK:
+        msg = lib().glsdm_last_error().decode()
+        if rc in (ERR_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE):
+            raise ValueError(f"{name}: {msg}")
+        raise NativeError(f"{name} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(t):
+    try:
+        return DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"GL-SDM native kernels support float32 and bfloat16, not {t.dtype}") from None
+
+
+def require_device(*tensors):
+    """Same contract as the reference's require_cuda (S/memory/backends/primitives.py:7-12):
+    contiguous tensors on a HIP device (ROCm torch reports them as CUDA), one device."""
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError("GL-SDM native kernels require contiguous CUDA (HIP) tensors")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError("GL-SDM native operands must share one device")
+    return device
+
+
+def version():
+    return lib().glsdm_version().decode()

@@ -1,0 +1,211 @@
+"""HIP backend of the GL-SDM memory operator: the native entry points in the
+shape of the reference's native backends (S/ = projects/gl-sdm/src/gl_sdm/):
+
+=========================  ===================================================
+this module                reference entry point it stands in for
+=========================  ===================================================
+``routed_snapshot_read``   ``S/memory/backends/urm.py:109-122``
+``snapshot_read``          ``S/memory/backends/urm.py:64-82``
+``route``                  ``S/memory/backends/token.py:85-114`` (lowest ties)
+``commit``                 ``S/memory/backends/commit.py:36-58``
+``absolute_addresses``     ``S/memory/routing.py:31-34``
+``gather_rows``            ``S/memory/routing.py:37-42``, ``primitives.py:15-20``
+``proposal_keys``          ``S/layers/global_layer.py:45,52-53``
+``score``                  ``S/layers/global_layer.py:26,42`` (per-head form)
+``require_cuda``           ``S/memory/backends/primitives.py:7-12``
+=========================  ===================================================
+
+All tensors are torch-allocated on the caller's current stream; the library
+never allocates device memory and never synchronises.  Forward only: inputs
+that require gradients are rejected (the backward pass is not built yet).
+"""
+import torch
+
+from ... import _native as N
+
+
+def require_cuda(*tensors):
+    return N.require_device(*tensors)
+
+
+def _no_grad(*tensors):
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise NotImplementedError("the HIP memory operator is forward-only; run it under torch.no_grad()")
+
+
+def _square_root(slots):
+    half = int(round(slots ** 0.5))
+    while half * half > slots:
+        half -= 1
+    while (half + 1) * (half + 1) <= slots:
+        half += 1
+    if half * half != slots:
+        raise ValueError("GL-SDM requires square slots and route sizes in [1, slots]")
+    return half
+
+
+def route(scores, count, tie="lowest"):
+    """Product-key route of fp32 scores ``[..., 2*half]`` -> (index int64, weights fp32) ``[..., count]``."""
+    _no_grad(scores)
+    scores = scores.float().contiguous() if scores.dtype != torch.float32 else scores
+    device = require_cuda(scores)
+    half = scores.shape[-1] // 2
+    if scores.shape[-1] != 2 * half or not 1 <= count <= half * half:
+        raise ValueError("GL-SDM routing needs [..., 2*half] scores and 1 <= count <= half**2")
+    index = torch.empty((*scores.shape[:-1], count), dtype=torch.int64, device=device)
+    weights = torch.empty((*scores.shape[:-1], count), dtype=torch.float32, device=device)
+    rows = scores.numel() // scores.shape[-1]
+    N.call("glsdm_route", N.ptr(scores), rows, half, count, N.TIES[tie], N.ptr(index), N.ptr(weights),
+           N.stream(device))
+    return index, weights
+
+
+def snapshot_read(values, index, weights, out_dtype=torch.float32):
+    """Weighted gather ``sum_j w_j * values[b, h, index_j]`` -> ``[B, T, H, D]``."""
+    _no_grad(values, weights)
+    device = require_cuda(values, index, weights)
+    B, H, S, D = values.shape
+    if index.ndim != 4 or index.shape[0] != B or index.shape[2] != H or weights.shape != index.shape:
+        raise ValueError("snapshot_read needs [B, T, H, width] int64 index and fp32 weights")
+    if index.dtype != torch.int64 or weights.dtype != torch.float32:
+        raise ValueError("snapshot_read needs int64 index and fp32 weights")
+    T, width = index.shape[1], index.shape[3]
+    out = torch.empty((B, T, H, D), dtype=out_dtype, device=device)
+    N.call("glsdm_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, width, N.ptr(index),
+           N.ptr(weights), N.ptr(out), N.dtype_code(out), N.stream(device))
+    return out
+
+
+def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="highest",
+                         out_dtype=torch.float32):
+    """Route fp32 scores ``[B, T, H, 2*half]`` and read the bank ``[B, H, half**2, D]``.
+
+    Returns ``(readings [B,T,H,D], index int64 [B,T,H,width] ascending, weights fp32)``.
+    ``allow_large_route`` is accepted for signature compatibility; every factor
+    extent up to 65535 is supported.
+    """
+    del allow_large_route
+    _no_grad(values, scores)
+    scores = scores if scores.dtype == torch.float32 else scores.float()
+    scores = scores.contiguous()
+    device = require_cuda(values, scores)
+    B, H, S, D = values.shape
+    if scores.ndim != 4 or scores.shape[0] != B or scores.shape[2] != H:
+        raise ValueError("routed_snapshot_read needs [B, T, H, 2*half] scores matching the bank")
+    half = _square_root(S)
+    if scores.shape[3] != 2 * half or not 1 <= width <= S:
+        raise ValueError("GL-SDM requires square slots and route sizes in [1, slots]")
+    T = scores.shape[1]
+    out = torch.empty((B, T, H, D), dtype=out_dtype, device=device)
+    index = torch.empty((B, T, H, width), dtype=torch.int64, device=device)
+    weights = torch.empty((B, T, H, width), dtype=torch.float32, device=device)
+    N.call("glsdm_route_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, N.ptr(scores), width,
+           N.TIES[tie], N.ptr(out), N.dtype_code(out), N.ptr(index), N.ptr(weights), N.stream(device))
+    return out, index, weights
+
+
+def score(queries, subkeys):
+    """Factor scores ``[B, T, H, L]`` fp32 from bf16 queries ``[B, T, H, dk]`` and sub-keys ``[H, L, dk]``."""
+    _no_grad(queries, subkeys)
+    device = require_cuda(queries, subkeys)
+    if queries.dtype != torch.bfloat16 or subkeys.dtype != torch.bfloat16:
+        raise ValueError("score needs bf16 queries and sub-keys")
+    B, T, H, dk = queries.shape
+    if subkeys.ndim != 3 or subkeys.shape[0] != H or subkeys.shape[2] != dk or subkeys.shape[1] % 2:
+        raise ValueError("score needs sub-keys [H, 2*half, dk] matching the queries")
+    L = subkeys.shape[1]
+    out = torch.empty((B, T, H, L), dtype=torch.float32, device=device)
+    N.call("glsdm_score", N.ptr(queries), N.ptr(subkeys), B, T, H, dk, L // 2, N.ptr(out), N.stream(device))
+    return out
+
+
+def absolute_addresses(values, index):
+    """``(b*H + h)*S + index`` for ``index [B, T, H, width]``."""
+    device = require_cuda(values, index)
+    B, H, S, _ = values.shape
+    if index.ndim != 4 or index.dtype != torch.int64 or index.shape[0] != B or index.shape[2] != H:
+        raise ValueError("absolute_addresses needs a [B, T, H, width] int64 index")
+    out = torch.empty_like(index)
+    N.call("glsdm_absolute_addresses", N.ptr(index), B, index.shape[1], H, index.shape[3], S, N.ptr(out),
+           N.stream(device))
+    return out
+
+
+def proposal_keys(values, index, offset, chunk_size, num_layers, layer_idx):
+    """Write addresses and collision keys ``addr*(C*L) + (offset + t)*L + layer``."""
+    device = require_cuda(values, index)
+    B, H, S, _ = values.shape
+    if index.ndim != 4 or index.dtype != torch.int64 or index.shape[0] != B or index.shape[2] != H:
+        raise ValueError("proposal_keys needs a [B, T, H, width] int64 index")
+    addresses = torch.empty_like(index)
+    keys = torch.empty_like(index)
+    N.call("glsdm_proposal_keys", N.ptr(index), B, index.shape[1], H, index.shape[3], S, offset, chunk_size,
+           num_layers, layer_idx, N.ptr(addresses), N.ptr(keys), N.stream(device))
+    return addresses, keys
+
+
+def gather_rows(values, index):
+    """Rows ``[B, T, H, width, D]`` of the bank at ``index [B, T, H, width]``."""
+    addr = absolute_addresses(values, index)
+    device = values.device
+    D = values.shape[-1]
+    out = torch.empty((*index.shape, D), dtype=values.dtype, device=device)
+    rows = values.numel() // D
+    N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), rows, D, N.ptr(addr), addr.numel(),
+           N.ptr(out), N.stream(device))
+    return out
+
+
+def _bits(n):
+    """Bits needed for the values 0 .. n-1."""
+    return max(int(n - 1).bit_length(), 0)
+
+
+def commit_workspace_bytes(entries, key_bits):
+    size = N.ctypes.c_size_t(0)
+    N.call("glsdm_commit_workspace_bytes", entries, key_bits, N.ctypes.byref(size))
+    return size.value
+
+
+def commit(memory, indices, deltas, keys=None, donate=False, key_bound=None, workspace=None, unique=None):
+    """Deterministic commit of ``deltas [E, D]`` at absolute rows ``indices [E]``.
+
+    ``memory`` is any contiguous tensor whose last dimension is D (e.g. the
+    ``[B, H, S, D]`` bank).  Returns the updated bank: a new tensor, or
+    ``memory`` itself updated in place when ``donate=True`` (the caller gives
+    up the old contents; no full-bank copy is made).
+
+    ``keys`` (int64 [E], default: the addresses) orders colliding deltas.
+    ``key_bound`` is an exclusive upper bound of the keys (all keys >= 0); when
+    omitted it is read from the keys with one device-to-host copy.
+    ``workspace`` (uint8 device tensor) and ``unique`` (int64 [1] device
+    counter, incremented by the number of touched rows) are optional.
+    """
+    _no_grad(memory, deltas)
+    device = require_cuda(memory, indices, deltas, keys)
+    if indices.dtype != torch.int64 or (keys is not None and keys.dtype != torch.int64):
+        raise ValueError("commit needs int64 addresses and keys")
+    D = memory.shape[-1]
+    E = indices.numel()
+    deltas = deltas.reshape(E, D) if deltas.numel() == E * D else None
+    if deltas is None or (keys is not None and keys.numel() != E):
+        raise ValueError("commit needs deltas [E, D] and keys [E] matching the addresses")
+    out = memory if donate else memory.clone()
+    if E == 0:
+        return out
+    rows = memory.numel() // D
+    key_min = 0
+    if keys is None:
+        key_bits = _bits(rows)
+    elif key_bound is not None:
+        key_bits = _bits(int(key_bound))
+    else:
+        lo, hi = (int(v) for v in torch.aminmax(keys))
+        key_min, key_bits = lo, _bits(hi - lo + 1)
+    need = commit_workspace_bytes(E, key_bits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    N.call("glsdm_commit", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(deltas),
+           N.dtype_code(deltas), N.ptr(keys), key_min, key_bits, E, N.ptr(workspace), workspace.numel(),
+           N.ptr(unique), N.stream(device))
+    return out

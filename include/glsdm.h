@@ -1,0 +1,167 @@
+/*
+ * glsdm.h -- C ABI of libglsdm.so, the MI355X (gfx950) implementation of
+ * GL-SDM's transactional sparse-memory operator: product-key routing, snapshot
+ * read and the deterministic buffered commit.
+ *
+ * Reference citations use S/ = projects/gl-sdm/src/gl_sdm/ in kreasof-ai/GL-SDM.
+ *
+ * Conventions (every entry point):
+ *   - Plain pointers to device memory and sizes; no C++ or framework types.
+ *   - Returns GLSDM_OK (0) or a negative status; glsdm_last_error() then holds
+ *     a message (thread-local).
+ *   - Asynchronous on the given HIP stream (hipStream_t passed as void*; NULL is
+ *     the null stream).  No host synchronisation, no device allocation: the
+ *     caller owns every buffer, including the commit workspace.
+ *   - Bank / value rows are row-major [rows, D] of dtype GLSDM_F32 or
+ *     GLSDM_BF16.  Index tensors are int64, weights and scores fp32.
+ *   - Out-of-range slots or addresses never fault: such route entries
+ *     contribute nothing to a read and such commit entries are dropped.
+ */
+#ifndef GLSDM_H
+#define GLSDM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLSDM_OK 0
+#define GLSDM_ERR_ARG (-1)         /* invalid argument or shape */
+#define GLSDM_ERR_UNSUPPORTED (-2) /* valid but outside the supported envelope */
+#define GLSDM_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+#define GLSDM_ERR_HIP (-4)         /* a HIP runtime call failed */
+
+#define GLSDM_F32 0
+#define GLSDM_BF16 1
+
+/* Tie rule for equal scores.  HIGHEST: the larger sub-key / slot index wins
+ * (the chunk path, S/memory/routing.py:4,15-17,21-23).  LOWEST: the smaller
+ * index wins (the token path, S/layers/router.py:45-55). */
+#define GLSDM_TIE_HIGHEST 0
+#define GLSDM_TIE_LOWEST 1
+
+/* Library version string. */
+const char *glsdm_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char *glsdm_last_error(void);
+
+/*
+ * Product-key route of fp32 factor scores.
+ *   scores  [rows, 2*half] fp32: factor 0 in columns [0, half), factor 1 in [half, 2*half)
+ *   index   [rows, width] int64 out: chosen slots i*half + j, ascending
+ *   weights [rows, width] fp32 out: softmax of the chosen slots' summed scores
+ * Per row: per factor the min(width, half) best sub-keys, their grid of fp32
+ * sums, the best `width` grid cells, ascending slot order, softmax.
+ * Envelope: 1 <= half <= 65535, 1 <= width <= 64, width <= half*half.
+ * Replaces: the route half of S/memory/routing.py:10-26 (torch_routed_read) and
+ * of S/memory/backends/urm.py:109-122 (routed_snapshot_read), with tie HIGHEST;
+ * S/memory/backends/token.py:85-114 (_Route / route) and S/layers/router.py:39-61, with
+ * tie LOWEST.
+ */
+int glsdm_route(const float *scores, int64_t rows, int32_t half, int32_t width, int32_t tie,
+                int64_t *index, float *weights, void *stream);
+
+/*
+ * Snapshot read from supplied routes.
+ *   bank    [B, H, S, D] of bank_dtype (flattened rows (b*H + h)*S + slot)
+ *   index   [B, T, H, width] int64 local slots in [0, S); weights same shape fp32
+ *   out     [B, T, H, D] of out_dtype: sum_j weights[j] * bank_row[j], fp32 accumulation
+ * Envelope: D <= 64 * 8 * (16 / sizeof(bank element)) when D is a multiple of the
+ * 16-byte vector, D <= 512 otherwise; width <= 1024.
+ * Replaces: S/memory/routing.py:27-28 (weighted gather of torch_routed_read),
+ * S/memory/backends/urm.py:64-82 (snapshot_read) and the native branch of
+ * S/memory/transactions.py:28-35 (read).
+ */
+int glsdm_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+               int64_t T, int32_t width, const int64_t *index, const float *weights,
+               void *out, int32_t out_dtype, void *stream);
+
+/*
+ * Route then read (glsdm_route followed by glsdm_read on the same stream).
+ *   scores [B, T, H, 2*half] fp32 with half*half == S.
+ * Replaces: S/memory/backends/urm.py:109-122 (routed_snapshot_read) and
+ * S/memory/routing.py:10-28 (torch_routed_read).
+ */
+int glsdm_route_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S,
+                     int64_t D, int64_t T, const float *scores, int32_t width, int32_t tie,
+                     void *out, int32_t out_dtype, int64_t *index, float *weights, void *stream);
+
+/*
+ * Address scoring on bf16 MFMA: scores[b,t,h,c] = sum_e queries[b,t,h,e] * subkeys[h,c,e]
+ * with fp32 accumulation, c in [0, 2*half).  queries [B,T,H,dk] bf16,
+ * subkeys [H, 2*half, dk] bf16, scores [B,T,H,2*half] fp32 out.
+ * Envelope: dk a multiple of 32, 2*half a multiple of 64.
+ * Replaces: the factor-score projection feeding routed_read,
+ * S/layers/global_layer.py:26 (router.q) and :42 (router.k), in its per-head
+ * sub-key form.
+ */
+int glsdm_score(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                int32_t dk, int32_t half, float *scores, void *stream);
+
+/*
+ * Bytes of workspace glsdm_commit needs for `entries` deltas whose keys span
+ * `key_bits` bits (keys - key_min < 2^key_bits).
+ */
+int glsdm_commit_workspace_bytes(int64_t entries, int32_t key_bits, size_t *bytes);
+
+/*
+ * Deterministic buffered commit, in place on `bank`.
+ *   bank      [rows, D] of bank_dtype, updated in place
+ *   addresses [entries] int64 absolute rows
+ *   deltas    [entries, D] of delta_dtype
+ *   keys      [entries] int64 collision order, or NULL for keys = addresses;
+ *             keys must place equal addresses next to each other once sorted
+ *             (true for keys = addresses and for address-major keys such as
+ *             addr*(C*L) + pos*L + layer)
+ *   key_min, key_bits: every key k satisfies 0 <= k - key_min < 2^key_bits
+ *   unique_out: optional int64 device counter; the number of touched rows is
+ *             added to it (NULL to skip)
+ * Result: for every address a, bank[a] = round(bank[a] + s_a) where s_a is the
+ * fp32 sum, starting from 0, of a's deltas in stable ascending key order;
+ * round is identity for fp32 and round-to-nearest-even for bf16.  No floating
+ * point atomics: the result is bitwise reproducible.
+ * Replaces: S/memory/transactions.py:69-97 (commit; torch branch order) and
+ * S/memory/backends/commit.py:36-58 (_Commit.forward), without the full-bank
+ * clone (callers that need the old bank copy it first).
+ */
+int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                 const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                 const int64_t *keys, int64_t key_min, int32_t key_bits, int64_t entries,
+                 void *workspace, size_t workspace_bytes, int64_t *unique_out, void *stream);
+
+/*
+ * Absolute addresses (b*H + h)*S + index[b,t,h,j] for index [B,T,H,width].
+ * Replaces: S/memory/routing.py:31-34 (absolute_addresses) and
+ * S/memory/transactions.py:13-16 (addresses, with requests = arange(B)).
+ */
+int glsdm_absolute_addresses(const int64_t *index, int64_t B, int64_t T, int64_t H,
+                             int32_t width, int64_t S, int64_t *out, void *stream);
+
+/*
+ * Write addresses and collision keys of one proposal, index [B,T,H,width]:
+ *   addresses = (b*H + h)*S + index[b,t,h,j]
+ *   keys      = addresses*(chunk*layers) + (position_offset + t)*layers + layer
+ * so collisions order by (address, position in the chunk, layer).
+ * Replaces: S/layers/global_layer.py:45 (absolute_addresses) and :52-53
+ * (keys = addresses * (chunk_size * num_layers) + positions * num_layers + layer_idx).
+ */
+int glsdm_proposal_keys(const int64_t *index, int64_t B, int64_t T, int64_t H, int32_t width,
+                        int64_t S, int64_t position_offset, int64_t chunk, int64_t layers,
+                        int64_t layer, int64_t *addresses, int64_t *keys, void *stream);
+
+/*
+ * Row gather out[i] = bank[addresses[i]] for n addresses; out has bank_dtype.
+ * Replaces: S/memory/routing.py:37-42 (gather_rows) and
+ * S/memory/backends/primitives.py:15-20 (_gather).
+ */
+int glsdm_gather_rows(const void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                      const int64_t *addresses, int64_t n, void *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLSDM_H */

@@ -1,0 +1,63 @@
+"""The C-ABI library loads and exports every entry point include/glsdm.h declares;
+argument validation answers before any device work (no GPU needed)."""
+import ctypes
+
+import pytest
+
+from glsdm import _native as N
+from _util import header_functions
+
+
+def test_header_declares_the_expected_surface():
+    names = header_functions()
+    for required in ("glsdm_route", "glsdm_read", "glsdm_route_read", "glsdm_score", "glsdm_commit",
+                     "glsdm_commit_workspace_bytes", "glsdm_absolute_addresses", "glsdm_proposal_keys",
+                     "glsdm_gather_rows", "glsdm_version", "glsdm_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = N.lib()
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing
+    assert set(header_functions()) == set(N.SIGNATURES)
+
+
+def test_version():
+    assert "gfx950" in N.version()
+
+
+def _rc(name, *args):
+    return getattr(N.lib(), name)(*args)
+
+
+def test_route_rejects_bad_arguments_before_launch():
+    assert _rc("glsdm_route", None, 4, 8, 0, 0, None, None, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_route", None, 4, 8, 65, 0, None, None, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_route", None, 4, 2, 5, 0, None, None, None) == N.ERR_ARG    # width > slots
+    assert _rc("glsdm_route", None, 4, 8, 4, 7, None, None, None) == N.ERR_ARG    # tie
+    assert _rc("glsdm_route", None, 4, 8, 4, 0, None, None, None) == N.ERR_ARG    # null pointers
+    assert "null" in N.lib().glsdm_last_error().decode()
+    assert _rc("glsdm_route", None, 0, 8, 4, 0, None, None, None) == N.OK         # empty is a no-op
+
+
+def test_commit_workspace_contract():
+    size = ctypes.c_size_t(0)
+    assert _rc("glsdm_commit_workspace_bytes", 524288, 31, ctypes.byref(size)) == N.OK
+    assert size.value >= 2 * 8 * 524288
+    assert _rc("glsdm_commit_workspace_bytes", 1 << 40, 40, ctypes.byref(size)) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_commit", ctypes.c_void_p(1), 0, 16, 4, ctypes.c_void_p(1), ctypes.c_void_p(1), 0,
+               None, 0, 4, 8, None, 0, None, None) == N.ERR_WORKSPACE
+    assert _rc("glsdm_commit", None, 0, 16, 4, None, None, 0, None, 0, 4, 0, None, 0, None, None) == N.OK
+
+
+def test_read_and_score_envelopes():
+    assert _rc("glsdm_read", None, 0, 1, 1, 16, 5000, 1, 4, None, None, None, 0, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_score", None, None, 1, 1, 1, 48, 32, None, None) == N.ERR_UNSUPPORTED  # dk % 32
+    assert _rc("glsdm_score", None, None, 1, 1, 1, 64, 20, None, None) == N.ERR_UNSUPPORTED  # L % 64
+    assert _rc("glsdm_route_read", None, 0, 1, 1, 15, 8, 1, None, 4, 0, None, 0, None, None, None) == N.ERR_ARG
+
+
+def test_errors_become_python_exceptions():
+    with pytest.raises(ValueError, match="width"):
+        N.call("glsdm_route", None, 4, 8, 0, 0, None, None, None)

@@ -1,0 +1,113 @@
+"""HIP commit vs the oracle: bitwise for fp32 and bf16 banks (the summation
+order is the reference's), the reference's golden cancellation fixtures, and
+the commit invariants (untouched rows, repeatability, donation)."""
+import pytest
+import torch
+
+from oracle import c_oracle, torch_oracle
+from glsdm.memory import MemoryView, WriteProposal, merge, commit
+from glsdm.memory.backends import hip
+from _util import known_answers
+
+pytestmark = pytest.mark.gpu
+
+
+def test_commit_golden_fixtures(device):
+    ka = known_answers()
+    c = ka["commit_stable_collisions"]
+    view = MemoryView(torch.zeros(1, 1, c["rows"], 1, device=device))
+    p = WriteProposal(0, torch.tensor(c["addresses"], device=device),
+                      torch.tensor(c["deltas"], device=device)[:, None], view.lineage)
+    out = commit(view, merge(view, [p]))
+    assert out.values.flatten().tolist() == c["expect"]
+    assert out.version == 1 and out.lineage is view.lineage
+    assert view.values.abs().sum().item() == 0          # the old view is unchanged
+    with pytest.raises(ValueError, match="stale"):
+        commit(out, merge(view, [p]))
+
+    c = ka["commit_keyed_arrival_order"]
+    view = MemoryView(torch.zeros(1, 1, c["rows"], 1, device=device))
+    props = [WriteProposal(0, torch.tensor([a], device=device), torch.tensor([[d]], device=device),
+                           view.lineage, torch.tensor([k], device=device))
+             for a, d, k in zip(c["addresses"], c["deltas"], c["keys"])]
+    a = commit(view, merge(view, props))
+    b = commit(view, merge(view, [props[i] for i in c["permutation"]]))
+    assert torch.equal(a.values, b.values) and a.values.flatten()[3].item() == c["expect_row3"]
+
+    c = ka["commit_unrelated_addresses"]
+    view = MemoryView(torch.zeros(1, 1, c["rows"], 1, device=device))
+    p = WriteProposal(0, torch.tensor(c["addresses"], device=device),
+                      torch.tensor(c["deltas"], device=device)[:, None], view.lineage)
+    assert commit(view, merge(view, [p])).values[0, 0, 3, 0].item() == c["expect_row3"]
+
+
+def _case(rows, D, E, spread, seed, bank_dtype=torch.float32, delta_dtype=torch.float32, keyed=True):
+    g = torch.Generator().manual_seed(seed)
+    flat = torch.randn(rows, D, generator=g).to(bank_dtype)
+    addr = torch.randint(0, spread, (E,), generator=g)
+    delta = (torch.randn(E, D, generator=g) * 0.02).to(delta_dtype)
+    keys = addr * (E + 1) + torch.randperm(E, generator=g) if keyed else None
+    return flat, addr, delta, keys
+
+
+@pytest.mark.parametrize("keyed", [False, True])
+@pytest.mark.parametrize("rows,D,E,spread", [
+    (64, 8, 5, 4), (4096, 256, 8192, 4096), (1000, 128, 20000, 300), (50000, 128, 70000, 50000),
+    (67, 37, 300, 67), (10, 16, 3000, 3), (1, 4, 1, 1), (2048, 512, 4096, 64), (300, 2048, 600, 300),
+])
+def test_commit_fp32_bitwise(device, keyed, rows, D, E, spread):
+    flat, addr, delta, keys = _case(rows, D, E, spread, seed=rows + E, keyed=keyed)
+    unique = torch.zeros(1, dtype=torch.int64, device=device)
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device),
+                     None if keys is None else keys.to(device), unique=unique)
+    ref, n = c_oracle.commit(flat, addr, delta, keys)
+    assert torch.equal(out.cpu(), ref)
+    assert unique.item() == n
+
+
+@pytest.mark.parametrize("bank_dtype,delta_dtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                                    (torch.float32, torch.bfloat16)])
+def test_commit_mixed_precision_bitwise(device, bank_dtype, delta_dtype):
+    flat, addr, delta, keys = _case(8192, 128, 40000, 8192, seed=11, bank_dtype=bank_dtype, delta_dtype=delta_dtype)
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
+    ref = torch_oracle.commit(flat.float(), addr, delta.float(), keys).to(bank_dtype)
+    assert out.dtype == bank_dtype
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_commit_donate_repeat_and_untouched(device):
+    flat, addr, delta, keys = _case(5000, 64, 9000, 3000, seed=3)
+    base = flat.to(device)
+    first = hip.commit(base, addr.to(device), delta.to(device), keys.to(device))
+    for _ in range(3):
+        again = hip.commit(base, addr.to(device), delta.to(device), keys.to(device))
+        assert torch.equal(again, first)
+    assert torch.equal(base.cpu(), flat)                  # functional by default
+    donated = base.clone()
+    out = hip.commit(donated, addr.to(device), delta.to(device), keys.to(device), donate=True)
+    assert out.data_ptr() == donated.data_ptr() and torch.equal(out, first)
+    untouched = torch.ones(5000, dtype=torch.bool)
+    untouched[addr] = False
+    assert torch.equal(first.cpu()[untouched], flat[untouched])
+
+
+def test_commit_key_bound_and_offset_keys(device):
+    flat, addr, delta, _ = _case(700, 16, 5000, 700, seed=8)
+    keys = addr * 5000 + torch.arange(5000) - 12345          # negative keys: offset by their minimum
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
+    ref, _ = c_oracle.commit(flat, addr, delta, keys)
+    assert torch.equal(out.cpu(), ref)
+    pos = addr * 5000 + torch.arange(5000)
+    out2 = hip.commit(flat.to(device), addr.to(device), delta.to(device), pos.to(device), key_bound=700 * 5000)
+    ref2, _ = c_oracle.commit(flat, addr, delta, pos)
+    assert torch.equal(out2.cpu(), ref2)
+
+
+def test_commit_drops_out_of_range_addresses(device):
+    flat, addr, delta, _ = _case(100, 8, 500, 100, seed=4, keyed=False)
+    bad = addr.clone()
+    bad[::50] = 100                      # one past the end; keys = addresses, so they sort last
+    out = hip.commit(flat.to(device), bad.to(device), delta.to(device))
+    keep = bad < 100
+    ref, _ = c_oracle.commit(flat, bad[keep], delta[keep])
+    assert torch.equal(out.cpu(), ref)
