@@ -6,20 +6,25 @@
 // then old + sum.  No float atomics anywhere, so the result is bitwise
 // reproducible.
 //
-// Pipeline (all stream-ordered, no host sync):
-//   1. pack:    v[e] = (key[e] - key_min) << ebits | e, ebits = bits of E-1.
-//               Ordering the packed words orders by (key, entry) -- a stable
-//               key sort -- and the entry id rides along for free.
-//   2. radix:   LSD radix sort of the packed words over bits [ebits, ebits +
-//               key_bits) in 8-bit digits.  Each pass is histogram -> one-block
-//               exclusive scan -> stable scatter.  The entry bits below ebits
-//               are never sorted: they start in ascending order and every pass
-//               is stable.  Stable in-tile ranking uses wavefront ballots
-//               (match-any over the 8 digit bits) and per-wave LDS counters.
-//   3. segment: one lane group per sorted position; the first position of each
-//               address run walks the run in order, accumulating the deltas in
-//               fp32 registers, then read-modify-writes the bank row once.
-//               Exactly one group writes each touched row.
+// Pipeline (stream-ordered, no host sync, 3 + passes launches):
+//   1. prep:      zero the per-pass digit histograms, look-back words and tile
+//                 counters of the workspace (a fill kernel, safe under capture).
+//   2. pack+hist: v[e] = (key[e] - key_min) << ebits | e, ebits = bits of E-1,
+//                 and the digit histograms of every radix pass in one read.
+//                 Ordering the packed words orders by (key, entry): a stable
+//                 key sort, with the entry id riding along for free.
+//   3. passes:    LSD radix sort over bits [ebits, ebits + key_bits), 8-bit
+//                 digits, one kernel per pass: tiles take ids in launch order,
+//                 rank their items stably (wavefront ballots: match-any over the
+//                 8 digit bits, per-wave LDS counters), publish per-digit counts
+//                 and resolve their global offsets by decoupled look-back over
+//                 earlier tiles' published counts.  The entry bits below ebits
+//                 are never sorted: they start ascending and every pass is stable.
+//   4. segment:   a wavefront per 64 sorted positions loads entry ids and
+//                 addresses in parallel, finds run heads with a ballot, and its
+//                 lane groups each walk one run in order, summing the deltas in
+//                 fp32 registers, then read-modify-write that bank row once.
+//                 Exactly one lane group writes each touched row.
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -31,28 +36,42 @@ constexpr int SORT_ITEMS = 8;                           // per thread
 constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // 2048 entries
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // 512 consecutive entries per wave
-constexpr int SCAN_THREADS = 1024;
+constexpr int MAX_PASSES = 8;
+constexpr int64_t MAX_ENTRIES = (int64_t)1 << 30;       // look-back words hold 30-bit counts
+
+constexpr uint32_t LB_AGGREGATE = 1u << 30;             // tile's own count published
+constexpr uint32_t LB_PREFIX = 2u << 30;                // inclusive prefix published
+constexpr uint32_t LB_VALUE = LB_AGGREGATE - 1;
+constexpr uint32_t LB_SPIN_LIMIT = 1u << 22;            // bounded wait; exceeded only by a bug
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct CommitWorkspace {
     uint64_t *a, *b;
-    uint32_t *hist;
+    uint32_t *ghist;    // [MAX_PASSES][RADIX] global digit counts
+    uint32_t *status;   // [passes][tiles][RADIX] look-back words
+    uint32_t *counter;  // [MAX_PASSES] tile-id counters, then one error word
     int64_t tiles;
+    size_t status_words;
     size_t bytes;
 };
 
-static CommitWorkspace plan_workspace(void *base, int64_t entries)
+static CommitWorkspace plan_workspace(void *base, int64_t entries, int passes)
 {
     CommitWorkspace w;
     w.tiles = ceil_div(entries, SORT_TILE);
+    w.status_words = (size_t)passes * (size_t)w.tiles * RADIX;
     const size_t words = align256(sizeof(uint64_t) * (size_t)entries);
-    const size_t hist = align256(sizeof(uint32_t) * (size_t)RADIX * (size_t)w.tiles);
+    const size_t ghist = align256(sizeof(uint32_t) * MAX_PASSES * RADIX);
+    const size_t status = align256(sizeof(uint32_t) * w.status_words);
+    const size_t counter = align256(sizeof(uint32_t) * (MAX_PASSES + 1));
     char *p = static_cast<char *>(base);
     w.a = reinterpret_cast<uint64_t *>(p);
     w.b = reinterpret_cast<uint64_t *>(p + words);
-    w.hist = reinterpret_cast<uint32_t *>(p + 2 * words);
-    w.bytes = 2 * words + hist;
+    w.ghist = reinterpret_cast<uint32_t *>(p + 2 * words);
+    w.status = reinterpret_cast<uint32_t *>(p + 2 * words + ghist);
+    w.counter = reinterpret_cast<uint32_t *>(p + 2 * words + ghist + status);
+    w.bytes = 2 * words + ghist + status + counter;
     return w;
 }
 
@@ -63,77 +82,74 @@ static int entry_bits(int64_t entries)
     return b;
 }
 
-__global__ __launch_bounds__(256) void pack_kernel(const int64_t *__restrict__ keys,
-                                                   const int64_t *__restrict__ addresses,
-                                                   int64_t key_min, int ebits, int64_t n,
-                                                   uint64_t *__restrict__ out)
+static int pass_count(int key_bits) { return (key_bits + RADIX_BITS - 1) / RADIX_BITS; }
+
+__global__ __launch_bounds__(256) void commit_prep_kernel(uint32_t *__restrict__ ghist, uint32_t *__restrict__ status,
+                                                          int64_t status_words, uint32_t *__restrict__ counter)
 {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t i = tid; i < status_words; i += stride) status[i] = 0;
+    if (tid < MAX_PASSES * RADIX) ghist[tid] = 0;
+    if (tid < MAX_PASSES + 1) counter[tid] = 0;
+}
+
+__global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ keys,
+                                                        const int64_t *__restrict__ addresses, int64_t key_min,
+                                                        int ebits, int passes, int64_t n,
+                                                        uint64_t *__restrict__ out, uint32_t *__restrict__ ghist)
+{
+    __shared__ uint32_t h[MAX_PASSES][RADIX];
+    for (int p = 0; p < passes; ++p) h[p][threadIdx.x] = 0;
+    __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t k = (keys ? keys[i] : addresses[i]) - key_min;
-        out[i] = ((uint64_t)k << ebits) | (uint64_t)i;
+        const uint64_t v = ((uint64_t)k << ebits) | (uint64_t)i;
+        out[i] = v;
+        for (int p = 0; p < passes; ++p)
+            atomicAdd(&h[p][(uint32_t)(v >> (ebits + p * RADIX_BITS)) & (RADIX - 1)], 1u);
+    }
+    __syncthreads();
+    for (int p = 0; p < passes; ++p) {
+        const uint32_t c = h[p][threadIdx.x];
+        if (c) atomicAdd(&ghist[p * RADIX + threadIdx.x], c);
     }
 }
 
-__global__ __launch_bounds__(SORT_THREADS) void radix_hist_kernel(const uint64_t *__restrict__ in, int64_t n,
-                                                                  int shift, uint32_t *__restrict__ hist,
-                                                                  int64_t tiles)
-{
-    __shared__ uint32_t h[RADIX];
-    h[threadIdx.x] = 0;
-    __syncthreads();
-    const int64_t base = (int64_t)blockIdx.x * SORT_TILE;
-#pragma unroll
-    for (int k = 0; k < SORT_ITEMS; ++k) {
-        const int64_t i = base + k * SORT_THREADS + threadIdx.x;
-        if (i < n) atomicAdd(&h[(uint32_t)(in[i] >> shift) & (RADIX - 1)], 1u);
-    }
-    __syncthreads();
-    hist[(int64_t)threadIdx.x * tiles + blockIdx.x] = h[threadIdx.x];
-}
-
-// Exclusive scan of n counters in place, by one block.
-__global__ __launch_bounds__(SCAN_THREADS) void radix_scan_kernel(uint32_t *__restrict__ hist, int64_t n)
-{
-    __shared__ uint32_t part[SCAN_THREADS];
-    const int64_t per = ceil_div(n, SCAN_THREADS);
-    const int64_t lo = threadIdx.x * per;
-    const int64_t hi = lo + per < n ? lo + per : n;
-    uint32_t s = 0;
-    for (int64_t i = lo; i < hi; ++i) s += hist[i];
-    part[threadIdx.x] = s;
-    __syncthreads();
-    for (int off = 1; off < SCAN_THREADS; off <<= 1) {   // Hillis-Steele inclusive scan
-        const uint32_t x = threadIdx.x >= (unsigned)off ? part[threadIdx.x - off] : 0u;
-        __syncthreads();
-        part[threadIdx.x] += x;
-        __syncthreads();
-    }
-    uint32_t run = part[threadIdx.x] - s;
-    for (int64_t i = lo; i < hi; ++i) {
-        const uint32_t c = hist[i];
-        hist[i] = run;
-        run += c;
-    }
-}
-
-__global__ __launch_bounds__(SORT_THREADS) void radix_scatter_kernel(const uint64_t *__restrict__ in,
-                                                                     uint64_t *__restrict__ out, int64_t n,
-                                                                     int shift,
-                                                                     const uint32_t *__restrict__ offsets,
-                                                                     int64_t tiles)
+__global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *__restrict__ in,
+                                                                uint64_t *__restrict__ out, int64_t n, int shift,
+                                                                const uint32_t *__restrict__ ghist,
+                                                                uint32_t *__restrict__ status,
+                                                                uint32_t *__restrict__ counter,
+                                                                uint32_t *__restrict__ error)
 {
     __shared__ uint32_t cnt[SORT_WAVES][RADIX];
-    __shared__ uint32_t tile_base[RADIX];
+    __shared__ uint32_t base[RADIX];
+    __shared__ uint32_t scan[RADIX];
+    __shared__ uint32_t s_tile;
     const int tid = threadIdx.x;
+    if (tid == 0) s_tile = atomicAdd(counter, 1u);     // tile ids in the order tiles start
 #pragma unroll
     for (int w = 0; w < SORT_WAVES; ++w) cnt[w][tid] = 0;
-    tile_base[tid] = offsets[(int64_t)tid * tiles + blockIdx.x];
+    scan[tid] = ghist[tid];
     __syncthreads();
+    const int64_t tile = s_tile;
 
+    // exclusive prefix over digits of the global histogram (Hillis-Steele in LDS)
+    const uint32_t own = scan[tid];
+    for (int off = 1; off < RADIX; off <<= 1) {
+        const uint32_t x = tid >= off ? scan[tid - off] : 0u;
+        __syncthreads();
+        scan[tid] += x;
+        __syncthreads();
+    }
+    const uint32_t digit_base = scan[tid] - own;
+
+    // stable rank of each item within its wave's 512 consecutive entries
     const int wave = tid >> 6, lane = tid & 63;
     const uint64_t lt = (1ull << lane) - 1ull;
-    const int64_t start = (int64_t)blockIdx.x * SORT_TILE + (int64_t)wave * WAVE_ITEMS;
+    const int64_t start = tile * SORT_TILE + (int64_t)wave * WAVE_ITEMS;
     uint64_t v[SORT_ITEMS];
     uint32_t dig[SORT_ITEMS], pos[SORT_ITEMS];
 #pragma unroll
@@ -143,7 +159,6 @@ __global__ __launch_bounds__(SORT_THREADS) void radix_scatter_kernel(const uint6
         v[k] = valid ? in[i] : 0ull;
         const uint32_t d = (uint32_t)(v[k] >> shift) & (RADIX - 1);
         dig[k] = d;
-        // lanes of this wave holding the same digit, restricted to valid lanes
         uint64_t peers = __ballot(valid);
 #pragma unroll
         for (int bit = 0; bit < RADIX_BITS; ++bit) {
@@ -158,84 +173,143 @@ __global__ __launch_bounds__(SORT_THREADS) void radix_scatter_kernel(const uint6
         if (valid && before == 0) cnt[wave][d] = c + (uint32_t)__popcll(peers);
     }
     __syncthreads();
-    {   // exclusive prefix of the per-wave counts, per digit
-        uint32_t run = 0;
+
+    // thread `tid` owns digit `tid`: wave prefix, tile total, look-back
+    uint32_t total = 0;
 #pragma unroll
-        for (int w = 0; w < SORT_WAVES; ++w) {
-            const uint32_t x = cnt[w][tid];
-            cnt[w][tid] = run;
-            run += x;
-        }
+    for (int w = 0; w < SORT_WAVES; ++w) {
+        const uint32_t x = cnt[w][tid];
+        cnt[w][tid] = total;
+        total += x;
     }
+    uint32_t *word = status + tile * RADIX + tid;
+    uint32_t prefix = 0;
+    if (tile == 0) {
+        __hip_atomic_store(word, LB_PREFIX | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __hip_atomic_store(word, LB_AGGREGATE | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t *look = word - RADIX;
+        uint32_t spins = 0;
+        for (;;) {
+            const uint32_t s = __hip_atomic_load(look, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((s & ~LB_VALUE) == 0) {               // predecessor not published yet
+                if (++spins > LB_SPIN_LIMIT) { atomicOr(error, 1u); break; }
+                continue;
+            }
+            prefix += s & LB_VALUE;
+            if (s & LB_PREFIX) break;
+            look -= RADIX;                             // aggregate only: keep walking back
+        }
+        __hip_atomic_store(word, LB_PREFIX | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    base[tid] = digit_base + prefix;
     __syncthreads();
+
 #pragma unroll
     for (int k = 0; k < SORT_ITEMS; ++k) {
         const int64_t i = start + k * 64 + lane;
-        const int64_t dst = (int64_t)tile_base[dig[k]] + cnt[wave][dig[k]] + pos[k];
+        const int64_t dst = (int64_t)base[dig[k]] + cnt[wave][dig[k]] + pos[k];
         if (i < n && dst < n) out[dst] = v[k];   // dst < n always holds; the guard keeps a bug from faulting
     }
 }
 
+// One wavefront per 64 consecutive sorted positions; lane groups of `lpr` lanes
+// (one bank row each) walk the address runs that start in the wave's window.
 template <typename TB, typename TD, int VEC, int CH>
 __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int64_t rows, int64_t D,
                                                       const int64_t *__restrict__ addresses,
                                                       const TD *__restrict__ deltas,
                                                       const uint64_t *__restrict__ sorted, int64_t n,
                                                       uint64_t emask, int nv, int lpr,
-                                                      int64_t *__restrict__ unique_out)
+                                                      unsigned long long *__restrict__ unique_out)
 {
-    const int lane = threadIdx.x & 63;
-    const int ng = 64 / lpr;
-    const int grp = lane / lpr, li = lane % lpr;
-    const int64_t p = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * ng + grp;
-    if (p >= n) return;
-    // entry id -> address; an id outside [0, n) (impossible after a correct sort) reads as -1
-    auto addr_at = [&](int64_t q) -> int64_t {
-        const int64_t e = (int64_t)(sorted[q] & emask);
-        return e < n ? addresses[e] : -1;
-    };
-    const int64_t a = addr_at(p);
-    if (p > 0 && addr_at(p - 1) == a) return;   // not the first of its run
-    const bool in_range = a >= 0 && a < rows;
-
-    float acc[CH][VEC];
-#pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[c][e] = 0.0f;
-    int64_t q = p;
-    do {
-        const int64_t ent = (int64_t)(sorted[q] & emask);
-        if (in_range && ent < n) {
-            const TD *src = deltas + ent * D;
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int v = li + c * lpr;
-                if (v < nv) {
-                    float x[VEC];
-                    VecLoad<TD, VEC>::load(src + (int64_t)v * VEC, x);
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) acc[c][e] += x[e];
-                }
-            }
-        }
-        ++q;
-    } while (q < n && addr_at(q) == a);
-    if (!in_range) return;
-
-    TB *row = bank + a * D;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-        const int v = li + c * lpr;
-        if (v < nv) {
-            float old[VEC];
-            VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) old[e] = old[e] + acc[c][e];
-            VecStore<TB, VEC>::store(row + (int64_t)v * VEC, old);
+    __shared__ int64_t s_e[4][64];
+    __shared__ int64_t s_a[4][64];
+    __shared__ int s_head[4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
+    const int64_t p = p0 + lane;
+    const bool valid = p < n;
+    // entry id and address of this position (-1 for padding or a corrupt id)
+    int64_t e = valid ? (int64_t)(sorted[p] & emask) : n;
+    const int64_t a = e < n ? addresses[e] : -1;
+    int64_t prev = __shfl_up(a, 1);
+    if (lane == 0) {
+        prev = -2;
+        if (p0 > 0 && p0 - 1 < n) {
+            const int64_t ep = (int64_t)(sorted[p0 - 1] & emask);
+            prev = ep < n ? addresses[ep] : -1;
         }
     }
-    if (unique_out && li == 0) atomicAdd(reinterpret_cast<unsigned long long *>(unique_out), 1ull);
+    const bool head = valid && a != prev;
+    const uint64_t heads = __ballot(head);
+    s_e[wave][lane] = e;
+    s_a[wave][lane] = a;
+    if (head) s_head[wave][__popcll(heads & ((1ull << lane) - 1ull))] = lane;
+    const int nheads = __popcll(heads);
+    // rows this window will write: heads whose address is in range (one atomic per wave)
+    const uint64_t live = __ballot(head && a >= 0 && a < rows);
+    if (unique_out && lane == 0 && live) atomicAdd(unique_out, (unsigned long long)__popcll(live));
+    __syncthreads();
+
+    const int ng = 64 / lpr;
+    const int grp = lane / lpr, li = lane % lpr;
+    for (int r = grp; r < nheads; r += ng) {
+        const int h = s_head[wave][r];
+        const int64_t row_addr = s_a[wave][h];
+        const bool in_range = row_addr >= 0 && row_addr < rows;
+        TB *row = bank + (in_range ? row_addr : 0) * D;
+        float old[CH][VEC], acc[CH][VEC];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+#pragma unroll
+            for (int x = 0; x < VEC; ++x) acc[c][x] = 0.0f;
+            if (in_range && v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
+        }
+        int q = h;
+        for (;;) {
+            int64_t ent;
+            if (q < 64) {
+                ent = s_e[wave][q];
+            } else {
+                ent = (int64_t)(sorted[p0 + q] & emask);
+            }
+            if (in_range && ent < n) {
+                const TD *src = deltas + ent * D;
+#pragma unroll
+                for (int c = 0; c < CH; ++c) {
+                    const int v = li + c * lpr;
+                    if (v < nv) {
+                        float x[VEC];
+                        VecLoad<TD, VEC>::load(src + (int64_t)v * VEC, x);
+#pragma unroll
+                        for (int y = 0; y < VEC; ++y) acc[c][y] += x[y];
+                    }
+                }
+            }
+            ++q;
+            if (p0 + q >= n) break;
+            int64_t next;
+            if (q < 64) {
+                next = s_a[wave][q];
+            } else {
+                const int64_t en = (int64_t)(sorted[p0 + q] & emask);
+                next = en < n ? addresses[en] : -1;
+            }
+            if (next != row_addr) break;
+        }
+        if (!in_range) continue;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+            if (v < nv) {
+#pragma unroll
+                for (int x = 0; x < VEC; ++x) old[c][x] = old[c][x] + acc[c][x];
+                VecStore<TB, VEC>::store(row + (int64_t)v * VEC, old[c]);
+            }
+        }
+    }
 }
 
 template <typename TB, typename TD, int VEC>
@@ -243,16 +317,16 @@ static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t 
                              const void *deltas, const uint64_t *sorted, int64_t n, uint64_t emask,
                              const RowPlan &p, int64_t *unique_out, hipStream_t st)
 {
-    const int64_t per_block = 4 * (64 / p.lpr);
-    const dim3 grid((unsigned)ceil_div(n, per_block)), block(256);
+    const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
     TB *bk = static_cast<TB *>(bank);
     const TD *dl = static_cast<const TD *>(deltas);
+    auto *u = reinterpret_cast<unsigned long long *>(unique_out);
     switch (p.ch) {
-    case 1: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 1>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, unique_out); break;
-    case 2: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 2>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, unique_out); break;
+    case 1: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 1>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
+    case 2: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 2>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
     case 3:
-    case 4: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 4>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, unique_out); break;
-    default: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 8>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, unique_out); break;
+    case 4: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 4>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
+    default: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 8>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
     }
     return check_launch("segment_kernel");
 }
@@ -262,7 +336,7 @@ static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *
                             const void *deltas, const uint64_t *sorted, int64_t n, uint64_t emask,
                             int64_t *unique_out, hipStream_t st)
 {
-    // One vector width for both operands: the narrower type's 16-byte vector.
+    // One vector width for both operands: the wider type's 16-byte vector.
     constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
     const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(deltas)) & 15) == 0;
     if (D % VEC == 0 && aligned) {
@@ -283,9 +357,10 @@ extern "C" int glsdm_commit_workspace_bytes(int64_t entries, int32_t key_bits, s
 {
     if (!bytes) return fail(GLSDM_ERR_ARG, "commit_workspace_bytes: null output");
     if (entries < 0 || key_bits < 0 || key_bits > 63) return fail(GLSDM_ERR_ARG, "commit_workspace_bytes: bad arguments");
+    if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "commit: more than 2^30 entries");
     if (entries > 0 && key_bits + entry_bits(entries) > 64)
         return fail(GLSDM_ERR_UNSUPPORTED, "commit: key_bits %d + entry bits %d exceed 64", key_bits, entry_bits(entries));
-    *bytes = entries == 0 ? 0 : plan_workspace(nullptr, entries).bytes;
+    *bytes = entries == 0 ? 0 : plan_workspace(nullptr, entries, pass_count(key_bits)).bytes;
     return GLSDM_OK;
 }
 
@@ -298,32 +373,39 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
     if (!dtype_ok(bank_dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "commit: bad dtype");
     if (key_bits < 0 || key_bits > 63) return fail(GLSDM_ERR_ARG, "commit: key_bits must be in [0, 63]");
     if (entries == 0) return GLSDM_OK;
+    if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "commit: more than 2^30 entries");
     if (!bank || !addresses || !deltas) return fail(GLSDM_ERR_ARG, "commit: null pointer");
     if (D > 512 && D % 8 != 0) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld not a multiple of 8 above 512", (long long)D);
     if (D > 64 * 8 * 4) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld above 2048", (long long)D);
     const int ebits = entry_bits(entries);
     if (key_bits + ebits > 64)
         return fail(GLSDM_ERR_UNSUPPORTED, "commit: key_bits %d + entry bits %d exceed 64", key_bits, ebits);
-    CommitWorkspace ws = plan_workspace(workspace, entries);
+    const int passes = pass_count(key_bits);
+    CommitWorkspace ws = plan_workspace(workspace, entries, passes);
     if (!workspace || workspace_bytes < ws.bytes)
         return fail(GLSDM_ERR_WORKSPACE, "commit: workspace of %zu bytes needed, %zu given", ws.bytes, workspace_bytes);
     const hipStream_t st = as_stream(stream);
 
-    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), 65536);
-    hipLaunchKernelGGL(pack_kernel, dim3(pack_blocks), dim3(256), 0, st, keys, addresses, key_min, ebits, entries, ws.a);
-    int rc = check_launch("pack_kernel");
+    const unsigned prep_blocks = (unsigned)std::max<int64_t>(
+        std::min<int64_t>(ceil_div((int64_t)ws.status_words, 256), 4096), (MAX_PASSES * RADIX) / 256);
+    hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
+                       (int64_t)ws.status_words, ws.counter);
+    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), 1024);
+    hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, keys, addresses, key_min, ebits,
+                       passes, entries, ws.a, ws.ghist);
+    int rc = check_launch("commit pack");
     if (rc) return rc;
 
     uint64_t *src = ws.a, *dst = ws.b;
-    for (int shift = ebits; shift < ebits + key_bits; shift += RADIX_BITS) {
-        hipLaunchKernelGGL(radix_hist_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, src, entries, shift, ws.hist, ws.tiles);
-        hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(SCAN_THREADS), 0, st, ws.hist, (int64_t)RADIX * ws.tiles);
-        hipLaunchKernelGGL(radix_scatter_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, src, dst, entries, shift, ws.hist, ws.tiles);
-        if ((rc = check_launch("radix pass"))) return rc;
+    for (int p = 0; p < passes; ++p) {
+        hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, src, dst, entries,
+                           ebits + p * RADIX_BITS, ws.ghist + p * RADIX,
+                           ws.status + (size_t)p * ws.tiles * RADIX, ws.counter + p, ws.counter + MAX_PASSES);
+        if ((rc = check_launch("onesweep_kernel"))) return rc;
         uint64_t *t = src; src = dst; dst = t;
     }
 
-    const uint64_t emask = (ebits >= 64) ? ~0ull : ((1ull << ebits) - 1ull);
+    const uint64_t emask = (1ull << ebits) - 1ull;
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
         return launch_segment_t<float, float>(bank, rows, D, addresses, deltas, src, entries, emask, unique_out, st);
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
