@@ -5,8 +5,10 @@ epochs of C=512, H=8 heads, bank M=65536 slots per head (half=256, L=512
 factor scores per head), key dim dk=128, value dim D=128 (H*D = 1024), top-k
 16, bf16 bank/queries/deltas, fp32 accumulation.  One step = all 4 epochs of:
 
-  score(read queries) -> route -> snapshot read          (read path)
-  score(write queries) -> route -> proposal keys -> commit (write path)
+  score+route(read queries) -> snapshot read               (read path)
+  score+route(write queries) -> proposal keys -> commit     (write path)
+
+(score+route is one fused kernel: MFMA scores feed the top-k through LDS)
 
 with the bank updated in place at every 512-token clock (donated commit).
 Inputs are synthetic, generated on the CPU with a seeded generator and copied
@@ -58,8 +60,6 @@ class Pipeline:
         self.bank = bank.unsqueeze(0).expand(B, -1, -1, -1).contiguous().to(device)   # per-request replicas
         split = lambda x: [x[:, e * C:(e + 1) * C].contiguous().to(device) for e in range(self.epochs)]
         self.qr, self.qw, self.delta = split(qr), split(qw), split(delta)
-        L = 2 * half
-        self.scores = torch.empty(B, C, H, L, dtype=torch.float32, device=device)
         self.idx = torch.empty(B, C, H, k, dtype=torch.int64, device=device)
         self.w = torch.empty(B, C, H, k, dtype=torch.float32, device=device)
         self.out = torch.empty(B, C, H, D, dtype=torch.float32, device=device)
@@ -90,16 +90,12 @@ class Pipeline:
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.stream
         B, C, H, half, dk, D, k = (c[x] for x in ("B", "C", "H", "half", "dk", "D", "k"))
         S = half * half
-        self._timed("score", lambda: N.call("glsdm_score", p(self.qr[e]), p(self.keys), B, C, H, dk, half,
-                                            p(self.scores), st))
-        self._timed("route", lambda: N.call("glsdm_route", p(self.scores), B * C * H, half, k, N.TIE_HIGHEST,
-                                            p(self.idx), p(self.w), st))
+        self._timed("score_route", lambda: N.call("glsdm_score_route", p(self.qr[e]), p(self.keys), B, C, H, dk,
+                                                  half, k, N.TIE_HIGHEST, None, p(self.idx), p(self.w), st))
         self._timed("read", lambda: N.call("glsdm_read", p(self.bank), N.BF16, B, H, S, D, C, k, p(self.idx),
                                            p(self.w), p(self.out), N.F32, st))
-        self._timed("score", lambda: N.call("glsdm_score", p(self.qw[e]), p(self.keys), B, C, H, dk, half,
-                                            p(self.scores), st))
-        self._timed("route", lambda: N.call("glsdm_route", p(self.scores), B * C * H, half, k, N.TIE_HIGHEST,
-                                            p(self.widx), p(self.ww), st))
+        self._timed("score_route", lambda: N.call("glsdm_score_route", p(self.qw[e]), p(self.keys), B, C, H, dk,
+                                                  half, k, N.TIE_HIGHEST, None, p(self.widx), p(self.ww), st))
         self._timed("keys", lambda: N.call("glsdm_proposal_keys", p(self.widx), B, C, H, k, S, 0, C, 1, 0,
                                            p(self.addr), p(self.ckeys), st))
         self._timed("commit", lambda: N.call("glsdm_commit", p(self.bank), N.BF16, self.rows, D, p(self.addr),
@@ -221,16 +217,11 @@ def main():
         roof = {"kernel": "glsdm_commit (pack + radix passes + segment)", "bound": "hbm", "unit": "GB/s",
                 "peak": HBM_PEAK / 1e9}
         achieved = bytes_launch / t_launch / 1e9
-    elif dominant == "route":
-        # selection is VALU work on fp32 scores read from HBM
-        bytes_launch = cfg["B"] * cfg["C"] * cfg["H"] * (2 * cfg["half"] * 4 + cfg["k"] * 12)
-        t_launch = per_call["route"] * 1e-3
-        roof = {"kernel": "route_kernel (glsdm_route)", "bound": "hbm", "unit": "GB/s", "peak": HBM_PEAK / 1e9}
-        achieved = bytes_launch / t_launch / 1e9
     else:
+        # fused scoring + selection: the MFMA contraction is the only dense work
         flops = 2 * cfg["B"] * cfg["C"] * cfg["H"] * 2 * cfg["half"] * cfg["dk"]
-        t_launch = per_call["score"] * 1e-3
-        roof = {"kernel": "score_kernel (glsdm_score)", "bound": "mfma", "unit": "TFLOP/s",
+        t_launch = per_call["score_route"] * 1e-3
+        roof = {"kernel": "score_route_kernel (glsdm_score_route)", "bound": "mfma", "unit": "TFLOP/s",
                 "peak": MFMA_BF16_PEAK / 1e12}
         achieved = flops / t_launch / 1e12
         bytes_launch = None
@@ -252,7 +243,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded CPU generator, config-2 protocol)",
         "config": {"workload": "memory op, BASELINE configs[1]: B=8 T=2048 (4 epochs of 512) H=8 M=65536 "
-                               "dk=128 D=128 k=16 bf16, score+route+read+route+commit",
+                               "dk=128 D=128 k=16 bf16, fused score-route + read + fused score-route + keys + commit",
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
                    "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
                    "parallelism": "single GPU"},
@@ -261,8 +252,9 @@ def main():
                             "achieved_GBps": round(alg_total / rc_time / 1e9, 1),
                             "frac": round(alg_total / rc_time / HBM_PEAK, 4),
                             "op_frac": round(alg_total / (ms_step * 1e-3) / HBM_PEAK, 4)},
-        "scoring_mfma": {"flops_per_call": scoring_flops, "ms_per_call": round(per_call["score"], 5),
-                         "frac": round(scoring_flops / (per_call["score"] * 1e-3) / MFMA_BF16_PEAK, 4)},
+        "scoring_mfma": {"flops_per_call": scoring_flops, "ms_per_call": round(per_call["score_route"], 5),
+                         "frac": round(scoring_flops / (per_call["score_route"] * 1e-3) / MFMA_BF16_PEAK, 4),
+                         "note": "fused kernel: MFMA scoring + exact top-k selection in one launch"},
         "ms_per_call": {n: round(v, 5) for n, v in per_call.items()},
         "calls_per_step": calls,
         "unique_rows_per_epoch": unique,

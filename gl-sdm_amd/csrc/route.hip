@@ -16,77 +16,9 @@
 // group holds the row's exact top-K.  Factor lists go through LDS to the
 // candidate stage (kk*kk fp32 sums), which runs the same selection; the chosen
 // slots are sorted ascending and weighted by a softmax.
-#include "glsdm_internal.h"
+#include "select.h"
 
 namespace glsdm {
-
-template <int K, bool DESC>
-__device__ __forceinline__ void bitonic_sort(uint64_t (&v)[K])
-{
-#pragma unroll
-    for (int size = 2; size <= K; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-#pragma unroll
-            for (int i = 0; i < K; ++i) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool down = ((i & size) == 0) == DESC;
-                    const uint64_t a = v[i], b = v[j];
-                    const bool swap = down ? (a < b) : (a > b);
-                    v[i] = swap ? b : a;
-                    v[j] = swap ? a : b;
-                }
-            }
-        }
-    }
-}
-
-// t <- the K largest of t U c; both sorted descending, result sorted descending.
-template <int K>
-__device__ __forceinline__ void merge_top(uint64_t (&t)[K], const uint64_t (&c)[K])
-{
-#pragma unroll
-    for (int i = 0; i < K; ++i) t[i] = t[i] > c[K - 1 - i] ? t[i] : c[K - 1 - i];
-#pragma unroll
-    for (int stride = K >> 1; stride > 0; stride >>= 1) {
-#pragma unroll
-        for (int i = 0; i < K; ++i) {
-            const int j = i ^ stride;
-            if (j > i) {
-                const uint64_t a = t[i], b = t[j];
-                t[i] = a > b ? a : b;
-                t[j] = a > b ? b : a;
-            }
-        }
-    }
-}
-
-// Exact top-K keys of `n` elements produced by key_of(i), for the G-lane group
-// that lane g belongs to.  All lanes of the group return the same sorted list.
-template <int K, int G, typename KeyOf>
-__device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (&t)[K])
-{
-#pragma unroll
-    for (int i = 0; i < K; ++i) t[i] = 0;
-    for (int base = 0; base < n; base += G * K) {
-        uint64_t c[K];
-#pragma unroll
-        for (int q = 0; q < K; ++q) {
-            const int i = base + q * G + g;
-            c[q] = i < n ? key_of(i) : 0;
-        }
-        bitonic_sort<K, true>(c);
-        merge_top<K>(t, c);
-    }
-#pragma unroll
-    for (int s = 1; s < G; s <<= 1) {
-        uint64_t p[K];
-#pragma unroll
-        for (int q = 0; q < K; ++q) p[q] = shfl_xor_u64(t[q], s);
-        merge_top<K>(t, p);
-    }
-}
 
 template <int K, int G>
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ scores, int64_t rows,
@@ -123,56 +55,9 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ sc
     }
     __syncthreads();
 
-    // 2. best `width` cells of the kk x kk grid of fp32 sums
-    const uint32_t *i0 = s_idx[lr][0], *i1 = s_idx[lr][1];
-    const float *v0 = s_val[lr][0], *v1 = s_val[lr][1];
-    uint64_t t[K];
-    group_top<K, G>(kk * kk, g, [&](int c) {
-        const int i = c / kk, j = c - i * kk;
-        const float s = v0[i] + v1[j];
-        return rank_key(s, i0[i] * (uint32_t)half + i1[j], tie);
-    }, t);
-
-    // 3. chosen slots in ascending order, softmax over their sums
-    uint64_t u[K];
-#pragma unroll
-    for (int w = 0; w < K; ++w) {
-        if (w < width) {
-            const uint32_t slot = rank_index(t[w], tie);
-            const float s = order_value((uint32_t)(t[w] >> 32));
-            u[w] = ((uint64_t)slot << 32) | __float_as_uint(s);
-        } else {
-            u[w] = ~0ull;
-        }
-    }
-    bitonic_sort<K, false>(u);
-    float m = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < K; ++w) {
-        if (w < width) {
-            const float s = __uint_as_float((uint32_t)u[w]);
-            m = (s > m || s != s) ? s : m;
-        }
-    }
-    float e[K];
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < K; ++w) {
-        if (w < width) {
-            e[w] = expf(__uint_as_float((uint32_t)u[w]) - m);
-            total += e[w];
-        }
-    }
-    const float inv = 1.0f / total;
-    if (live) {
-#pragma unroll
-        for (int w = 0; w < K; ++w) {
-            if (w < width && w % G == g) {
-                index[row * width + w] = (int64_t)(u[w] >> 32);
-                weights[row * width + w] = e[w] * inv;
-            }
-        }
-    }
+    // 2. best `width` cells of the kk x kk grid of fp32 sums, ascending slots, softmax
+    finish_route<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, live,
+                       index + row * width, weights + row * width);
 }
 
 template <int K, int G>

@@ -1,0 +1,164 @@
+// Fused address scoring + product-key routing on gfx950.
+//
+// One block owns R = 256/G tokens of one head h.  For each factor the sub-key
+// columns are streamed in chunks of CW: the block's four wavefronts compute the
+// chunk's R x CW fp32 scores with v_mfma_f32_16x16x32_bf16 (query fragments
+// stay in registers for the whole kernel, sub-key fragments come from L2) and
+// drop them in LDS; then every G-lane group folds its token's CW scores into
+// its exact top-K lists (select.h).  Scores never reach HBM unless the caller
+// asks for them (scores_out, used for parity checks).  Blocks are numbered
+// head-fastest, so with 8 heads on 8 XCDs each XCD's L2 serves one head's
+// sub-key table.
+//
+// Semantics: scores as glsdm_score, routing as glsdm_route (the chosen slots,
+// weights and tie rule are identical on identical scores).
+#include "select.h"
+
+namespace glsdm {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+
+constexpr int KS_MAX = 8;   // dk <= 256
+
+template <int K, int G, int CW>
+__global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restrict__ q,
+                                                          const bf16_t *__restrict__ keys, int64_t N,
+                                                          int64_t H, int dk, int half, int width, int tie,
+                                                          float *__restrict__ scores_out,
+                                                          int64_t *__restrict__ index,
+                                                          float *__restrict__ weights)
+{
+    constexpr int R = 256 / G;       // tokens per block
+    constexpr int RT = R / 16;       // 16-row MFMA tiles
+    constexpr int WPR = 4 / RT;      // wavefronts per row tile
+    constexpr int CT = CW / 16;      // 16-column tiles per chunk
+    constexpr int CTW = CT / WPR;    // column tiles per wavefront
+    constexpr int SUB = CW / (G * K);
+    static_assert(RT >= 1 && RT <= 4 && CT % WPR == 0 && CTW >= 1 && SUB >= 1, "tiling");
+    __shared__ float s_sc[R][CW + 1];
+    __shared__ uint32_t s_idx[R][2][K];
+    __shared__ float s_val[R][2][K];
+
+    const int h = (int)(blockIdx.x % H);
+    const int64_t n0 = (int64_t)(blockIdx.x / H) * R;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rt = wave % RT, cshare = wave / RT;
+    const int li = lane & 15, kq = lane >> 4;
+    const int L = 2 * half;
+    const int ks = dk / 32;
+
+    // query fragments of this wavefront's 16-token tile, for all k-steps
+    int64_t qn = n0 + rt * 16 + li;
+    if (qn >= N) qn = N - 1;
+    const bf16_t *qrow = q + (qn * H + h) * dk + kq * 8;
+    bf16x8_t qa[KS_MAX];
+#pragma unroll
+    for (int s = 0; s < KS_MAX; ++s)
+        if (s < ks) qa[s] = *reinterpret_cast<const bf16x8_t *>(qrow + s * 32);
+
+    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int64_t row_n = n0 + lr;
+    const bool live = row_n < N;
+    const int kk = width < half ? width : half;
+
+    for (int f = 0; f < 2; ++f) {
+        uint64_t t[K];
+        list_clear<K>(t);
+        const bf16_t *fkeys = keys + ((int64_t)h * L + f * half) * dk + kq * 8;
+        for (int c0 = 0; c0 < half; c0 += CW) {
+#pragma unroll
+            for (int j = 0; j < CTW; ++j) {
+                const int ct = cshare * CTW + j;
+                const int col = c0 + ct * 16;
+                if (col >= half) continue;            // wave-uniform: half % 16 == 0
+                const bf16_t *krow = fkeys + (int64_t)(col + li) * dk;
+                floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < KS_MAX; ++s)
+                    if (s < ks)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            qa[s], *reinterpret_cast<const bf16x8_t *>(krow + s * 32), acc, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s_sc[rt * 16 + 4 * kq + r][ct * 16 + li] = acc[r];
+                if (scores_out) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t n = n0 + rt * 16 + 4 * kq + r;
+                        if (n < N) scores_out[(n * H + h) * L + f * half + col + li] = acc[r];
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int sub = 0; sub < SUB; ++sub) {
+                uint64_t c[K];
+#pragma unroll
+                for (int qi = 0; qi < K; ++qi) {
+                    const int i = (sub * K + qi) * G + g;
+                    const int col = c0 + i;
+                    c[qi] = col < half ? rank_key(s_sc[lr][i], (uint32_t)col, tie) : 0;
+                }
+                list_absorb<K>(t, c);
+            }
+            __syncthreads();
+        }
+        group_merge<K, G>(t);
+#pragma unroll
+        for (int i = 0; i < K; ++i) {
+            if (i % G == g && i < kk) {
+                s_idx[lr][f][i] = rank_index(t[i], tie);
+                s_val[lr][f][i] = order_value((uint32_t)(t[i] >> 32));
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t out_row = (live ? row_n : 0) * H + h;
+    finish_route<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, live,
+                       index + out_row * width, weights + out_row * width);
+}
+
+template <int K, int G, int CW>
+static int launch_score_route(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half,
+                              int width, int tie, float *scores_out, int64_t *index, float *weights,
+                              hipStream_t st)
+{
+    constexpr int R = 256 / G;
+    const int64_t blocks = ceil_div(N, R) * H;
+    if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: grid too large");
+    hipLaunchKernelGGL((score_route_kernel<K, G, CW>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(keys), N, H, dk, half,
+                       width, tie, scores_out, index, weights);
+    return check_launch("score_route_kernel");
+}
+
+}  // namespace glsdm
+
+using namespace glsdm;
+
+extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                                 int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
+                                 int64_t *index, float *weights, void *stream)
+{
+    if (B < 0 || T < 0 || H < 1 || dk < 1 || half < 1) return fail(GLSDM_ERR_ARG, "score_route: bad shape");
+    if (dk % 32 != 0 || dk > 32 * KS_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: dk=%d must be a multiple of 32 up to 256", dk);
+    if (half % 16 != 0 || half > 65535) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: half=%d must be a multiple of 16", half);
+    if (width < 1 || width > 64) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: width must be in [1, 64]");
+    if ((int64_t)width > (int64_t)half * half) return fail(GLSDM_ERR_ARG, "score_route: width exceeds slots");
+    if (tie != GLSDM_TIE_HIGHEST && tie != GLSDM_TIE_LOWEST) return fail(GLSDM_ERR_ARG, "score_route: bad tie rule");
+    const int64_t N = B * T;
+    if (N == 0) return GLSDM_OK;
+    if (!queries || !subkeys || !index || !weights) return fail(GLSDM_ERR_ARG, "score_route: null pointer");
+    if (((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(subkeys)) & 15) != 0)
+        return fail(GLSDM_ERR_UNSUPPORTED, "score_route: queries and sub-keys must be 16-byte aligned");
+    const hipStream_t st = as_stream(stream);
+    switch (pow2_ceil(width)) {
+    case 1: return launch_score_route<1, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 2: return launch_score_route<2, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 4: return launch_score_route<4, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 8: return launch_score_route<8, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 16: return launch_score_route<16, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 32: return launch_score_route<32, 8, 256>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    default: return launch_score_route<64, 8, 512>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    }
+}

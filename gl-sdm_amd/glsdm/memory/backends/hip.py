@@ -119,6 +119,28 @@ def score(queries, subkeys):
     return out
 
 
+def score_route(queries, subkeys, width, tie="highest", export_scores=False):
+    """Fused MFMA scoring + route: bf16 queries ``[B,T,H,dk]`` and sub-keys ``[H,L,dk]``
+    -> ``(index int64 [B,T,H,width], weights fp32, scores fp32 [B,T,H,L] or None)``."""
+    _no_grad(queries, subkeys)
+    device = require_cuda(queries, subkeys)
+    if queries.dtype != torch.bfloat16 or subkeys.dtype != torch.bfloat16:
+        raise ValueError("score_route needs bf16 queries and sub-keys")
+    B, T, H, dk = queries.shape
+    if subkeys.ndim != 3 or subkeys.shape[0] != H or subkeys.shape[2] != dk or subkeys.shape[1] % 2:
+        raise ValueError("score_route needs sub-keys [H, 2*half, dk] matching the queries")
+    L = subkeys.shape[1]
+    half = L // 2
+    if not 1 <= width <= half * half:
+        raise ValueError("GL-SDM requires square slots and route sizes in [1, slots]")
+    index = torch.empty((B, T, H, width), dtype=torch.int64, device=device)
+    weights = torch.empty((B, T, H, width), dtype=torch.float32, device=device)
+    scores = torch.empty((B, T, H, L), dtype=torch.float32, device=device) if export_scores else None
+    N.call("glsdm_score_route", N.ptr(queries), N.ptr(subkeys), B, T, H, dk, half, width, N.TIES[tie],
+           N.ptr(scores), N.ptr(index), N.ptr(weights), N.stream(device))
+    return index, weights, scores
+
+
 def absolute_addresses(values, index):
     """``(b*H + h)*S + index`` for ``index [B, T, H, width]``."""
     device = require_cuda(values, index)

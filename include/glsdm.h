@@ -102,6 +102,21 @@ int glsdm_score(const void *queries, const void *subkeys, int64_t B, int64_t T, 
                 int32_t dk, int32_t half, float *scores, void *stream);
 
 /*
+ * Fused scoring + route: the factor scores of glsdm_score are produced on MFMA
+ * and fed to the glsdm_route selection through LDS, without an HBM round trip.
+ *   queries [B,T,H,dk] bf16, subkeys [H, 2*half, dk] bf16 (16-byte aligned)
+ *   index [B,T,H,width] int64 out (ascending slots), weights fp32 out
+ *   scores_out: NULL, or [B,T,H,2*half] fp32 to also export the scores
+ * Results equal glsdm_route applied to the exported scores, bit for bit.
+ * Envelope: dk a multiple of 32 up to 256, half a multiple of 16, width <= 64.
+ * Replaces: S/layers/global_layer.py:26-27 and :42-43 (router.q/k projection
+ * followed by routing.routed_read's route, S/memory/routing.py:10-26).
+ */
+int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                      int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
+                      int64_t *index, float *weights, void *stream);
+
+/*
  * Bytes of workspace glsdm_commit needs for `entries` deltas whose keys span
  * `key_bits` bits (keys - key_min < 2^key_bits).
  */

@@ -1,0 +1,57 @@
+"""Fused MFMA scoring + route: the route is bit-exact against the oracle on the
+exported scores, the exported scores match a float64 contraction, and the
+result does not depend on whether scores are exported."""
+import pytest
+import torch
+
+from oracle import c_oracle, torch_oracle
+from glsdm.memory.backends import hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, T, H, dk, half, seed, clusters=False):
+    g = torch.Generator().manual_seed(seed)
+    norm = torch.nn.functional.normalize
+    k = norm(torch.randn(H, 2 * half, dk, generator=g), dim=-1)
+    if clusters:   # near-duplicate sub-keys: many close and equal scores
+        k = norm(k[:, :4].repeat(1, half // 2, 1) + 1e-3 * torch.randn(H, 2 * half, dk, generator=g), dim=-1)
+    q = norm(torch.randn(B, T, H, dk, generator=g), dim=-1)
+    return q.bfloat16(), k.bfloat16()
+
+
+@pytest.mark.parametrize("tie", ["highest", "lowest"])
+@pytest.mark.parametrize("B,T,H,dk,half,width", [
+    (8, 64, 8, 128, 256, 16),      # config 2 geometry
+    (2, 100, 1, 64, 64, 8),        # config 1 geometry, ragged token count
+    (1, 40, 1, 128, 1024, 32),     # config 3 geometry
+    (2, 17, 2, 32, 16, 4), (1, 33, 3, 96, 48, 5), (1, 20, 1, 256, 32, 64), (1, 9, 2, 64, 16, 1),
+    (1, 18, 2, 64, 32, 2), (1, 70, 1, 128, 512, 8),
+])
+def test_fused_route_matches_oracle_on_exported_scores(device, tie, B, T, H, dk, half, width):
+    q, k = _inputs(B, T, H, dk, half, seed=B * T + half + width)
+    idx, w, scores = hip.score_route(q.to(device), k.to(device), width, tie, export_scores=True)
+    ref = torch.einsum("bthe,hce->bthc", q.double(), k.double())
+    torch.testing.assert_close(scores.cpu().double(), ref, atol=1e-5, rtol=1e-5)
+    ridx, rw = c_oracle.route(scores.cpu(), width, tie)
+    assert torch.equal(idx.cpu(), ridx)
+    torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
+    idx2, w2, none = hip.score_route(q.to(device), k.to(device), width, tie)
+    assert none is None and torch.equal(idx2, idx) and torch.equal(w2, w)
+
+
+@pytest.mark.parametrize("tie", ["highest", "lowest"])
+def test_fused_route_with_duplicate_subkeys(device, tie):
+    q, k = _inputs(2, 64, 2, 64, 64, seed=5, clusters=True)
+    idx, w, scores = hip.score_route(q.to(device), k.to(device), 16, tie, export_scores=True)
+    ridx, rw = torch_oracle.route(scores.cpu(), 16, tie)
+    assert torch.equal(idx.cpu(), ridx)
+    torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
+
+
+def test_fused_route_equals_unfused(device):
+    q, k = _inputs(4, 128, 8, 128, 256, seed=9)
+    idx, w, _ = hip.score_route(q.to(device), k.to(device), 16)
+    s = hip.score(q.to(device), k.to(device))
+    idx2, w2 = hip.route(s, 16, "highest")
+    assert torch.equal(idx, idx2) and torch.equal(w, w2)
