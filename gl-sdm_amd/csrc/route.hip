@@ -20,7 +20,7 @@
 
 namespace glsdm {
 
-template <int K, int G>
+template <int K, int G, bool PAIR>
 __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ scores, int64_t rows,
                                                     int half, int width, int tie,
                                                     int64_t *__restrict__ index,
@@ -29,44 +29,65 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ sc
     constexpr int RPB = 256 / G;
     __shared__ uint32_t s_idx[RPB][2][K];
     __shared__ float s_val[RPB][2][K];
+    __shared__ uint16_t s_pairs[STAIR_MAX];
 
     const int lr = threadIdx.x / G;
     const int g = threadIdx.x % G;
     const int64_t row = (int64_t)blockIdx.x * RPB + lr;
     const bool live = row < rows;
     const int64_t r = live ? row : rows - 1;
-    const float *src = scores + r * 2 * (int64_t)half;
+    const float *f0 = scores + r * 2 * (int64_t)half;
+    const float *f1 = f0 + half;
     const int kk = width < half ? width : half;
+    const int npairs = staircase_build(s_pairs, kk, width);
 
-    // 1. per-factor top-kk sub-keys (stashed in LDS for the candidate grid)
+    // 1. per-factor top-kk sub-keys (both factors in the same pass unless K = 64)
+    bool finite = true;
+    if constexpr (PAIR) {
+        uint64_t t0[K], t1[K];
+        list_clear<K>(t0);
+        list_clear<K>(t1);
+        for (int base = 0; base < half; base += G * K) {
+            uint64_t c0[K], c1[K];
 #pragma unroll
-    for (int f = 0; f < 2; ++f) {
-        const float *fs = src + f * half;
-        uint64_t t[K];
-        group_top<K, G>(half, g, [&](int i) { return rank_key(fs[i], (uint32_t)i, tie); }, t);
-#pragma unroll
-        for (int i = 0; i < K; ++i) {
-            if (i % G == g && i < kk) {
-                const uint32_t id = rank_index(t[i], tie);
-                s_idx[lr][f][i] = id;
-                s_val[lr][f][i] = fs[id];
+            for (int q = 0; q < K; ++q) {
+                const int i = base + q * G + g;
+                c0[q] = i < half ? rank_key(f0[i], (uint32_t)i, tie) : 0;
+                c1[q] = i < half ? rank_key(f1[i], (uint32_t)i, tie) : 0;
             }
+            list_absorb<K>(t0, c0);
+            list_absorb<K>(t1, c1);
+        }
+        group_merge2<K, G>(t0, t1);
+        const bool fa = stash_factor<K, G>(t0, kk, tie, g, s_idx[lr][0], s_val[lr][0]);
+        const bool fb = stash_factor<K, G>(t1, kk, tie, g, s_idx[lr][1], s_val[lr][1]);
+        finite = fa && fb;
+    } else {
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const float *fs = f ? f1 : f0;
+            uint64_t t0[K];
+            group_top<K, G>(half, g, [&](int i) { return rank_key(fs[i], (uint32_t)i, tie); }, t0);
+            const bool fa = stash_factor<K, G>(t0, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
+            finite = finite && fa;
         }
     }
     __syncthreads();
 
     // 2. best `width` cells of the kk x kk grid of fp32 sums, ascending slots, softmax
-    finish_route<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, live,
-                       index + row * width, weights + row * width);
+    uint64_t t[K];
+    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
+                        npairs, finite, t);
+    finish_route<K, G>(t, width, tie, g, live, index + row * width, weights + row * width);
 }
 
-template <int K, int G>
+template <int K, int G, bool PAIR = (K < 64)>
 static int launch_route(const float *scores, int64_t rows, int half, int width, int tie,
                         int64_t *index, float *weights, hipStream_t st)
 {
     constexpr int RPB = 256 / G;
     const int64_t blocks = ceil_div(rows, RPB);
-    hipLaunchKernelGGL((route_kernel<K, G>), dim3((unsigned)blocks), dim3(256), 0, st, scores, rows,
+    hipLaunchKernelGGL((route_kernel<K, G, PAIR>), dim3((unsigned)blocks), dim3(256), 0, st, scores, rows,
                        half, width, tie, index, weights);
     return check_launch("route_kernel");
 }

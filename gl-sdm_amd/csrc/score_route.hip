@@ -1,8 +1,8 @@
 // Fused address scoring + product-key routing on gfx950.
 //
-// One block owns R = 256/G tokens of one head h.  For each factor the sub-key
-// columns are streamed in chunks of CW: the block's four wavefronts compute the
-// chunk's R x CW fp32 scores with v_mfma_f32_16x16x32_bf16 (query fragments
+// One block owns R = 256/G tokens of one head h.  The sub-key columns of both
+// factors (one factor at a time for K = 64, to fit LDS) are streamed in chunks
+// of CW: the block's four wavefronts compute the chunk's R x CW fp32 scores with v_mfma_f32_16x16x32_bf16 (query fragments
 // stay in registers for the whole kernel, sub-key fragments come from L2) and
 // drop them in LDS; then every G-lane group folds its token's CW scores into
 // its exact top-K lists (select.h).  Scores never reach HBM unless the caller
@@ -21,7 +21,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 constexpr int KS_MAX = 8;   // dk <= 256
 
-template <int K, int G, int CW>
+template <int K, int G, int CW, bool PAIR>
 __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restrict__ q,
                                                           const bf16_t *__restrict__ keys, int64_t N,
                                                           int64_t H, int dk, int half, int width, int tie,
@@ -32,13 +32,16 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     constexpr int R = 256 / G;       // tokens per block
     constexpr int RT = R / 16;       // 16-row MFMA tiles
     constexpr int WPR = 4 / RT;      // wavefronts per row tile
-    constexpr int CT = CW / 16;      // 16-column tiles per chunk
-    constexpr int CTW = CT / WPR;    // column tiles per wavefront
+    constexpr int CT = CW / 16;      // 16-column tiles per chunk and factor
+    constexpr int CTW = CT / WPR;    // column tiles per wavefront and factor
     constexpr int SUB = CW / (G * K);
+    constexpr int LDW = CW + 4;      // padded LDS row (keeps 16-byte alignment)
+    constexpr int NF = PAIR ? 2 : 1; // factors per pass over the sub-keys
     static_assert(RT >= 1 && RT <= 4 && CT % WPR == 0 && CTW >= 1 && SUB >= 1, "tiling");
-    __shared__ float s_sc[R][CW + 1];
+    __shared__ __attribute__((aligned(16))) float s_sc[NF][R][LDW];
     __shared__ uint32_t s_idx[R][2][K];
     __shared__ float s_val[R][2][K];
+    __shared__ uint16_t s_pairs[STAIR_MAX];
 
     const int h = (int)(blockIdx.x % H);
     const int64_t n0 = (int64_t)(blockIdx.x / H) * R;
@@ -47,6 +50,12 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     const int li = lane & 15, kq = lane >> 4;
     const int L = 2 * half;
     const int ks = dk / 32;
+
+    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int64_t row_n = n0 + lr;
+    const bool live = row_n < N;
+    const int kk = width < half ? width : half;
+    const int npairs = staircase_build(s_pairs, kk, width);
 
     // query fragments of this wavefront's 16-token tile, for all k-steps
     int64_t qn = n0 + rt * 16 + li;
@@ -57,68 +66,79 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     for (int s = 0; s < KS_MAX; ++s)
         if (s < ks) qa[s] = *reinterpret_cast<const bf16x8_t *>(qrow + s * 32);
 
-    const int lr = threadIdx.x / G, g = threadIdx.x % G;
-    const int64_t row_n = n0 + lr;
-    const bool live = row_n < N;
-    const int kk = width < half ? width : half;
-
-    for (int f = 0; f < 2; ++f) {
-        uint64_t t[K];
-        list_clear<K>(t);
-        const bf16_t *fkeys = keys + ((int64_t)h * L + f * half) * dk + kq * 8;
+    const bf16_t *hkeys = keys + (int64_t)h * L * dk + kq * 8;
+    bool finite = true;
+    for (int fp = 0; fp < 2; fp += NF) {
+        uint64_t ta[K], tb[K];
+        list_clear<K>(ta);
+        if constexpr (PAIR) list_clear<K>(tb);
         for (int c0 = 0; c0 < half; c0 += CW) {
+            // MFMA: the pass's factors' scores of columns [c0, c0 + CW) for the block's R tokens
 #pragma unroll
-            for (int j = 0; j < CTW; ++j) {
-                const int ct = cshare * CTW + j;
-                const int col = c0 + ct * 16;
-                if (col >= half) continue;            // wave-uniform: half % 16 == 0
-                const bf16_t *krow = fkeys + (int64_t)(col + li) * dk;
-                floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+            for (int fi = 0; fi < NF; ++fi) {
+                const int f = fp + fi;
 #pragma unroll
-                for (int s = 0; s < KS_MAX; ++s)
-                    if (s < ks)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            qa[s], *reinterpret_cast<const bf16x8_t *>(krow + s * 32), acc, 0, 0, 0);
+                for (int j = 0; j < CTW; ++j) {
+                    const int ct = cshare * CTW + j;
+                    const int col = c0 + ct * 16;
+                    if (col >= half) continue;            // wave-uniform: half % 16 == 0
+                    const bf16_t *krow = hkeys + (int64_t)(f * half + col + li) * dk;
+                    floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s_sc[rt * 16 + 4 * kq + r][ct * 16 + li] = acc[r];
-                if (scores_out) {
+                    for (int s = 0; s < KS_MAX; ++s)
+                        if (s < ks)
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                qa[s], *reinterpret_cast<const bf16x8_t *>(krow + s * 32), acc, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int64_t n = n0 + rt * 16 + 4 * kq + r;
-                        if (n < N) scores_out[(n * H + h) * L + f * half + col + li] = acc[r];
+                    for (int r = 0; r < 4; ++r) s_sc[fi][rt * 16 + 4 * kq + r][ct * 16 + li] = acc[r];
+                    if (scores_out) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t n = n0 + rt * 16 + 4 * kq + r;
+                            if (n < N) scores_out[(n * H + h) * L + f * half + col + li] = acc[r];
+                        }
                     }
                 }
             }
             __syncthreads();
+            // selection: lane g of a token folds K contiguous columns per factor into its lists
 #pragma unroll
             for (int sub = 0; sub < SUB; ++sub) {
-                uint64_t c[K];
+                const int first = (sub * G + g) * K;
+                uint64_t a[K], b[K];
 #pragma unroll
                 for (int qi = 0; qi < K; ++qi) {
-                    const int i = (sub * K + qi) * G + g;
-                    const int col = c0 + i;
-                    c[qi] = col < half ? rank_key(s_sc[lr][i], (uint32_t)col, tie) : 0;
+                    const int col = c0 + first + qi;
+                    const bool in = col < half;
+                    a[qi] = in ? rank_key(s_sc[0][lr][first + qi], (uint32_t)col, tie) : 0;
+                    if constexpr (PAIR) b[qi] = in ? rank_key(s_sc[NF - 1][lr][first + qi], (uint32_t)col, tie) : 0;
                 }
-                list_absorb<K>(t, c);
+                list_absorb<K>(ta, a);
+                if constexpr (PAIR) list_absorb<K>(tb, b);
             }
             __syncthreads();
         }
-        group_merge<K, G>(t);
-#pragma unroll
-        for (int i = 0; i < K; ++i) {
-            if (i % G == g && i < kk) {
-                s_idx[lr][f][i] = rank_index(t[i], tie);
-                s_val[lr][f][i] = order_value((uint32_t)(t[i] >> 32));
-            }
+        if constexpr (PAIR) {
+            group_merge2<K, G>(ta, tb);
+            const bool fa = stash_factor<K, G>(ta, kk, tie, g, s_idx[lr][0], s_val[lr][0]);
+            const bool fb = stash_factor<K, G>(tb, kk, tie, g, s_idx[lr][1], s_val[lr][1]);
+            finite = fa && fb;
+        } else {
+            group_merge<K, G>(ta);
+            const bool fa = stash_factor<K, G>(ta, kk, tie, g, s_idx[lr][fp], s_val[lr][fp]);
+            finite = finite && fa;
         }
     }
     __syncthreads();
+
+    uint64_t t[K];
+    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
+                        npairs, finite, t);
     const int64_t out_row = (live ? row_n : 0) * H + h;
-    finish_route<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, live,
-                       index + out_row * width, weights + out_row * width);
+    finish_route<K, G>(t, width, tie, g, live, index + out_row * width, weights + out_row * width);
 }
 
-template <int K, int G, int CW>
+template <int K, int G, int CW, bool PAIR>
 static int launch_score_route(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half,
                               int width, int tie, float *scores_out, int64_t *index, float *weights,
                               hipStream_t st)
@@ -126,7 +146,7 @@ static int launch_score_route(const void *q, const void *keys, int64_t N, int64_
     constexpr int R = 256 / G;
     const int64_t blocks = ceil_div(N, R) * H;
     if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: grid too large");
-    hipLaunchKernelGGL((score_route_kernel<K, G, CW>), dim3((unsigned)blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR>), dim3((unsigned)blocks), dim3(256), 0, st,
                        static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(keys), N, H, dk, half,
                        width, tie, scores_out, index, weights);
     return check_launch("score_route_kernel");
@@ -153,12 +173,12 @@ extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64
         return fail(GLSDM_ERR_UNSUPPORTED, "score_route: queries and sub-keys must be 16-byte aligned");
     const hipStream_t st = as_stream(stream);
     switch (pow2_ceil(width)) {
-    case 1: return launch_score_route<1, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 2: return launch_score_route<2, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 4: return launch_score_route<4, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 8: return launch_score_route<8, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 16: return launch_score_route<16, 4, 64>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 32: return launch_score_route<32, 8, 256>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    default: return launch_score_route<64, 8, 512>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 1: return launch_score_route<1, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 2: return launch_score_route<2, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 4: return launch_score_route<4, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 8: return launch_score_route<8, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 16: return launch_score_route<16, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 32: return launch_score_route<32, 8, 256, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    default: return launch_score_route<64, 8, 512, false>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
     }
 }

@@ -4,10 +4,20 @@
 // descending top-K list of keys in registers (K a power of two).  Elements
 // arrive in chunks of K per lane: a chunk is sorted by a bitonic network and
 // merged into the list by a bitonic merge that keeps the K largest.  The G
-// lists are finally merged by a butterfly over __shfl_xor, after which every
-// lane of the group holds the row's exact top-K.  Keys are distinct (the index
-// is part of the key), so "the K largest keys" is well defined and equals the
-// reference's chain of stable argsorts.
+// lists are finally merged by a butterfly (DPP quad permutes for the two
+// innermost levels, __shfl_xor beyond), after which every lane of the group
+// holds the row's exact top-K.  Keys are distinct (the index is part of the
+// key), so "the K largest keys" is well defined and equals the reference's
+// chain of stable argsorts.
+//
+// Candidate stage: with both factor lists sorted, cell (i, j) of the sum grid
+// is dominated by the (i+1)(j+1)-1 cells (i' <= i, j' <= j), whose fp32 sums
+// are >= its own (rounding is monotone).  The selection therefore runs on the
+// staircase P = {(i, j): (i+1)(j+1) <= width} only, and then *verifies* that
+// every cell outside P scores strictly below the width-th pick: per grid row
+// the first excluded cell bounds all later ones, so one check per row suffices.
+// Ties at the boundary, infinities or NaN among the factor scores send the row
+// to the full-grid selection, so the result is exact in every case.
 #pragma once
 
 #include "glsdm_internal.h"
@@ -71,17 +81,55 @@ __device__ __forceinline__ void list_absorb(uint64_t (&t)[K], uint64_t (&c)[K])
     merge_top<K>(t, c);
 }
 
+// Value of lane (lane ^ S) for S in {1, 2} through a DPP quad permute, else a shuffle.
+template <int S>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v)
+{
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    if constexpr (S == 1) {
+        lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+        hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (S == 2) {
+        lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+        hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0x4E, 0xF, 0xF, false);
+    } else {
+        lo = (uint32_t)__shfl_xor((int)lo, S);
+        hi = (uint32_t)__shfl_xor((int)hi, S);
+    }
+    return ((uint64_t)hi << 32) | lo;
+}
+
+template <int K, int S>
+__device__ __forceinline__ void butterfly_level(uint64_t (&t)[K])
+{
+    uint64_t p[K];
+#pragma unroll
+    for (int q = 0; q < K; ++q) p[q] = lane_xor_u64<S>(t[q]);
+    merge_top<K>(t, p);
+}
+
 // Butterfly merge of the G lane lists of a group (G a power of two <= 64).
 template <int K, int G>
 __device__ __forceinline__ void group_merge(uint64_t (&t)[K])
 {
-#pragma unroll
-    for (int s = 1; s < G; s <<= 1) {
-        uint64_t p[K];
-#pragma unroll
-        for (int q = 0; q < K; ++q) p[q] = shfl_xor_u64(t[q], s);
-        merge_top<K>(t, p);
-    }
+    if constexpr (G > 1) butterfly_level<K, 1>(t);
+    if constexpr (G > 2) butterfly_level<K, 2>(t);
+    if constexpr (G > 4) butterfly_level<K, 4>(t);
+    if constexpr (G > 8) butterfly_level<K, 8>(t);
+    if constexpr (G > 16) butterfly_level<K, 16>(t);
+    if constexpr (G > 32) butterfly_level<K, 32>(t);
+}
+
+// Two independent lists merged level by level (more independent work per level).
+template <int K, int G>
+__device__ __forceinline__ void group_merge2(uint64_t (&t)[K], uint64_t (&u)[K])
+{
+    if constexpr (G > 1) { butterfly_level<K, 1>(t); butterfly_level<K, 1>(u); }
+    if constexpr (G > 2) { butterfly_level<K, 2>(t); butterfly_level<K, 2>(u); }
+    if constexpr (G > 4) { butterfly_level<K, 4>(t); butterfly_level<K, 4>(u); }
+    if constexpr (G > 8) { butterfly_level<K, 8>(t); butterfly_level<K, 8>(u); }
+    if constexpr (G > 16) { butterfly_level<K, 16>(t); butterfly_level<K, 16>(u); }
+    if constexpr (G > 32) { butterfly_level<K, 32>(t); butterfly_level<K, 32>(u); }
 }
 
 // Exact top-K keys of `n` elements produced by key_of(i), for the G-lane group
@@ -102,23 +150,78 @@ __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (
     group_merge<K, G>(t);
 }
 
-// Candidate stage and output of one route row.  i0/v0 and i1/v1 hold the
-// kk = min(width, half) best sub-keys of the two factors (indices and scores);
-// all G lanes of the group call this and lane g writes outputs w % G == g.
+// ------------------------------------------------------------------ staircase
+
+constexpr int STAIR_MAX = 280;   // |P| for width 64 (sum over n <= 64 of floor(64 / n))
+
+// Builds the staircase cells (i << 8 | j) of P for (kk, width) in LDS; every
+// thread of the block calls it, the caller synchronises before use.
+__device__ __forceinline__ int staircase_build(uint16_t *pairs, int kk, int width)
+{
+    const int i = threadIdx.x;
+    int total = 0, offset = 0;
+    for (int r = 0; r < kk; ++r) {
+        const int len = min(kk, width / (r + 1));
+        if (r < i) offset += len;
+        total += len;
+    }
+    if (i < kk) {
+        const int len = min(kk, width / (i + 1));
+        for (int j = 0; j < len; ++j) pairs[offset + j] = (uint16_t)((i << 8) | j);
+    }
+    return total;
+}
+
+// Best `width` cells (top-K list, descending keys) of the kk x kk sum grid of
+// the factor lists i0/v0 and i1/v1 (sorted descending by rank key).
 template <int K, int G>
-__device__ __forceinline__ void finish_route(const uint32_t *i0, const float *v0, const uint32_t *i1,
-                                             const float *v1, int half, int width, int tie, int g, bool live,
-                                             int64_t *index_row, float *weight_row)
+__device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v0, const uint32_t *i1,
+                                              const float *v1, int half, int width, int tie, int g,
+                                              const uint16_t *pairs, int npairs, bool finite,
+                                              uint64_t (&t)[K])
 {
     const int kk = width < half ? width : half;
-    uint64_t t[K];
-    group_top<K, G>(kk * kk, g, [&](int c) {
-        const int i = c / kk, j = c - i * kk;
+    auto cell = [&](int i, int j) {
         const float s = v0[i] + v1[j];
         return rank_key(s, i0[i] * (uint32_t)half + i1[j], tie);
-    }, t);
+    };
+    bool exact = false;
+    if (finite && npairs >= width) {
+        group_top<K, G>(npairs, g, [&](int c) {
+            const int pr = pairs[c];
+            return cell(pr >> 8, pr & 0xFF);
+        }, t);
+        // verify: the first excluded cell of each grid row scores strictly below the width-th pick
+        uint32_t tau = 0;
+#pragma unroll
+        for (int w = 0; w < K; ++w)
+            if (w == width - 1) tau = (uint32_t)(t[w] >> 32);
+        bool ok = true;
+        for (int i = g; i < kk; i += G) {
+            const int j = min(kk, width / (i + 1));
+            if (j < kk) ok = ok && order_bits(v0[i] + v1[j]) < tau;
+        }
+        // all G lanes of the group must agree
+        uint64_t bad = __ballot(!ok);
+        const int lane = threadIdx.x & 63;
+        const uint64_t mine = ((G >= 64) ? ~0ull : ((1ull << G) - 1ull)) << (lane & ~(G - 1));
+        exact = (bad & mine) == 0;
+    }
+    if (!exact) {
+        group_top<K, G>(kk * kk, g, [&](int c) {
+            const int i = c / kk;
+            return cell(i, c - i * kk);
+        }, t);
+    }
+}
 
-    // chosen slots in ascending order, softmax over their sums
+// Output stage of one route row from its candidate list t (top-K, descending):
+// chosen slots in ascending order, softmax over their sums; lane g of the
+// group writes the outputs w with w % G == g.
+template <int K, int G>
+__device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, int tie, int g, bool live,
+                                             int64_t *index_row, float *weight_row)
+{
     uint64_t u[K];
 #pragma unroll
     for (int w = 0; w < K; ++w) {
@@ -158,6 +261,27 @@ __device__ __forceinline__ void finish_route(const uint32_t *i0, const float *v0
             }
         }
     }
+}
+
+// Stashes the top-kk of a factor list (indices and scores) for the candidate
+// stage; returns whether all kk scores are finite.
+template <int K, int G>
+__device__ __forceinline__ bool stash_factor(const uint64_t (&t)[K], int kk, int tie, int g, uint32_t *idx,
+                                             float *val)
+{
+    bool finite = true;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+        if (i < kk) {
+            const float v = order_value((uint32_t)(t[i] >> 32));
+            finite = finite && (fabsf(v) <= 3.402823466e38f);
+            if (i % G == g) {
+                idx[i] = rank_index(t[i], tie);
+                val[i] = v;
+            }
+        }
+    }
+    return finite;
 }
 
 }  // namespace glsdm
