@@ -33,6 +33,17 @@ MFMA_BF16_PEAK = 2.5e15    # FLOP/s dense bf16
 
 CFG = dict(B=8, T=2048, C=512, H=8, half=256, dk=128, D=128, k=16)
 
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this
+# workload, scaled by a 256 MiB copy measured in the same run (FETCH x 1.9998,
+# WRITE x 1.0); source: profiles/glsdm_kernels.config2.hbm-traffic.md.  Re-measured
+# whenever a kernel of the path changes.
+TRAFFIC_PER_LAUNCH = {
+    "score_route": (4972.2 * 1.9998 + 6144.0) * 1024,
+    "read": (67336.2 * 1.9998 + 16384.0) * 1024,
+    "commit": ((10.7 + 2069.7 + 4 * 2525.5 + 138558.9) * 1.9998
+               + (1032.1 + 6301.7 + 4 * 4863.4 + 120899.2)) * 1024,
+}
+
 
 def make_inputs(cfg, seed=0):
     """Seeded CPU generation in a fixed order, then bf16 (config-2 protocol)."""
@@ -172,6 +183,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the timed region, copy 256 MiB device-to-device 3 times (a kernel of known "
+                         "traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -225,7 +239,9 @@ def main():
                 "peak": MFMA_BF16_PEAK / 1e12}
         achieved = flops / t_launch / 1e12
         bytes_launch = None
-    roof.update({"achieved": round(achieved, 1), "frac": round(achieved / roof["peak"], 4), "traffic": None})
+    traffic = TRAFFIC_PER_LAUNCH.get(dominant)
+    roof.update({"achieved": round(achieved, 1), "frac": round(achieved / roof["peak"], 4),
+                 "traffic": None if traffic is None else int(traffic)})
 
     scoring_flops = 2 * cfg["B"] * cfg["C"] * cfg["H"] * 2 * cfg["half"] * cfg["dk"]
     rc_time = epochs * (per_call["read"] + per_call["commit"]) * 1e-3
@@ -259,6 +275,13 @@ def main():
         "calls_per_step": calls,
         "unique_rows_per_epoch": unique,
     }
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_calibration_bytes"] = src.numel()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
     print(json.dumps(result))
