@@ -32,7 +32,13 @@ namespace glsdm {
 constexpr int RADIX_BITS = 8;
 constexpr int RADIX = 1 << RADIX_BITS;
 constexpr int SORT_THREADS = 256;
-constexpr int SORT_ITEMS = 8;                           // per thread
+#ifndef GLSDM_SORT_ITEMS
+#define GLSDM_SORT_ITEMS 8
+#endif
+#ifndef GLSDM_PACK_BLOCKS
+#define GLSDM_PACK_BLOCKS 128
+#endif
+constexpr int SORT_ITEMS = GLSDM_SORT_ITEMS;            // per thread
 constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // 2048 entries
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // 512 consecutive entries per wave
@@ -390,7 +396,7 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
         std::min<int64_t>(ceil_div((int64_t)ws.status_words, 256), 4096), (MAX_PASSES * RADIX) / 256);
     hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
                        (int64_t)ws.status_words, ws.counter);
-    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), 1024);
+    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), GLSDM_PACK_BLOCKS);
     hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, keys, addresses, key_min, ebits,
                        passes, entries, ws.a, ws.ghist);
     int rc = check_launch("commit pack");

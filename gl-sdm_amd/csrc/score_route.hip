@@ -2,9 +2,11 @@
 //
 // One block owns R = 256/G tokens of one head h.  The sub-key columns of both
 // factors (one factor at a time for K = 64, to fit LDS) are streamed in chunks
-// of CW: the block's four wavefronts compute the chunk's R x CW fp32 scores with v_mfma_f32_16x16x32_bf16 (query fragments
-// stay in registers for the whole kernel, sub-key fragments come from L2) and
-// drop them in LDS; then every G-lane group folds its token's CW scores into
+// of CW: the block stages the chunk's sub-key rows in LDS once (padded rows;
+// for K <= 16, the larger lists need the LDS themselves), its four wavefronts
+// compute the chunk's R x CW fp32 scores with v_mfma_f32_16x16x32_bf16 (query
+// fragments stay in registers for the whole kernel) and drop them in LDS;
+// then every G-lane group folds its token's CW scores into
 // its exact top-K lists (select.h).  Scores never reach HBM unless the caller
 // asks for them (scores_out, used for parity checks).  Blocks are numbered
 // head-fastest, so with 8 heads on 8 XCDs each XCD's L2 serves one head's
@@ -21,7 +23,22 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 constexpr int KS_MAX = 8;   // dk <= 256
 
-template <int K, int G, int CW, bool PAIR>
+// Orders LDS traffic between the lanes that produced a score chunk and the lanes
+// that select from it: the wavefront itself when every wavefront owns its own
+// 16 tokens end to end, else the whole block.
+template <bool WAVE_LOCAL>
+__device__ __forceinline__ void chunk_sync()
+{
+    if constexpr (WAVE_LOCAL) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+        __syncthreads();
+    }
+}
+
+template <int K, int G, int CW, bool PAIR, int KSM, bool STAGE>
 __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restrict__ q,
                                                           const bf16_t *__restrict__ keys, int64_t N,
                                                           int64_t H, int dk, int half, int width, int tie,
@@ -35,13 +52,28 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     constexpr int CT = CW / 16;      // 16-column tiles per chunk and factor
     constexpr int CTW = CT / WPR;    // column tiles per wavefront and factor
     constexpr int SUB = CW / (G * K);
-    constexpr int LDW = CW + 4;      // padded LDS row (keeps 16-byte alignment)
+    constexpr int LDW = CW + 4;      // padded LDS score row (keeps 16-byte alignment)
     constexpr int NF = PAIR ? 2 : 1; // factors per pass over the sub-keys
+    constexpr int LDK = KSM * 32 + 8;              // padded LDS sub-key row (bf16), breaks bank aliasing
+    constexpr int VPR = KSM * 4;                   // 16-byte pieces per sub-key row at the largest dk
+    constexpr int PIECES = (NF * CW * VPR + 255) / 256;   // staged pieces per thread and chunk
+    constexpr int SKN = STAGE ? NF : 1, SKC = STAGE ? CW : 1, SKL = STAGE ? LDK : 8;
+    // With G = 4 the 16-token MFMA tile of wavefront w is exactly the 16 tokens its
+    // lanes select for, so no other wavefront touches its score rows.
+    constexpr bool WAVE_LOCAL = (RT == 4 && WPR == 1 && G == 4);
     static_assert(RT >= 1 && RT <= 4 && CT % WPR == 0 && CTW >= 1 && SUB >= 1, "tiling");
-    __shared__ __attribute__((aligned(16))) float s_sc[NF][R][LDW];
-    __shared__ uint32_t s_idx[R][2][K];
-    __shared__ float s_val[R][2][K];
+    // With both factors in one pass the score chunks are dead once the chunk loop
+    // ends, so the factor lists of the candidate stage reuse their LDS (a block
+    // barrier separates the two); one factor per pass keeps them apart.
+    constexpr int SC_WORDS = NF * R * LDW, LIST_WORDS = 2 * R * 2 * K;
+    constexpr int LIST_AT = PAIR ? 0 : SC_WORDS;
+    constexpr int BUF_WORDS = (LIST_AT + LIST_WORDS > SC_WORDS) ? LIST_AT + LIST_WORDS : SC_WORDS;
+    __shared__ __attribute__((aligned(16))) float s_buf[BUF_WORDS];
+    __shared__ __attribute__((aligned(16))) bf16_t s_k[SKN][SKC][SKL];
     __shared__ uint16_t s_pairs[STAIR_MAX];
+    auto s_sc = reinterpret_cast<float (*)[R][LDW]>(s_buf);
+    auto s_idx = reinterpret_cast<uint32_t (*)[2][K]>(s_buf + LIST_AT);
+    auto s_val = reinterpret_cast<float (*)[2][K]>(s_buf + LIST_AT + R * 2 * K);
 
     const int h = (int)(blockIdx.x % H);
     const int64_t n0 = (int64_t)(blockIdx.x / H) * R;
@@ -50,6 +82,7 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     const int li = lane & 15, kq = lane >> 4;
     const int L = 2 * half;
     const int ks = dk / 32;
+    const int vpr = dk / 8;          // 16-byte pieces per sub-key row
 
     const int lr = threadIdx.x / G, g = threadIdx.x % G;
     const int64_t row_n = n0 + lr;
@@ -61,18 +94,39 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     int64_t qn = n0 + rt * 16 + li;
     if (qn >= N) qn = N - 1;
     const bf16_t *qrow = q + (qn * H + h) * dk + kq * 8;
-    bf16x8_t qa[KS_MAX];
+    bf16x8_t qa[KSM];
 #pragma unroll
-    for (int s = 0; s < KS_MAX; ++s)
+    for (int s = 0; s < KSM; ++s)
         if (s < ks) qa[s] = *reinterpret_cast<const bf16x8_t *>(qrow + s * 32);
 
-    const bf16_t *hkeys = keys + (int64_t)h * L * dk + kq * 8;
+    const bf16_t *hkeys = keys + (int64_t)h * L * dk;
+    // cooperative staging of a chunk's sub-key rows in LDS: piece p of this
+    // thread is (factor, column, 16-byte slice) = decode(threadIdx.x + 256 * p)
+    auto stage_chunk = [&](int fp, int c0) {
+        if constexpr (STAGE) {
+#pragma unroll
+            for (int p = 0; p < PIECES; ++p) {
+                const int id = threadIdx.x + 256 * p;
+                const int fi = id / (CW * vpr), rem = id - fi * (CW * vpr);
+                const int col = rem / vpr, sl = rem - col * vpr;
+                if (fi < NF && c0 + col < half)
+                    *reinterpret_cast<uint4 *>(&s_k[fi][col][sl * 8]) = *reinterpret_cast<const uint4 *>(
+                        hkeys + (int64_t)((fp + fi) * half + c0 + col) * dk + sl * 8);
+            }
+        }
+    };
+
     bool finite = true;
     for (int fp = 0; fp < 2; fp += NF) {
         uint64_t ta[K], tb[K];
         list_clear<K>(ta);
         if constexpr (PAIR) list_clear<K>(tb);
         for (int c0 = 0; c0 < half; c0 += CW) {
+            if constexpr (STAGE) {
+                __syncthreads();                  // every wavefront is done with the previous s_k
+                stage_chunk(fp, c0);
+                __syncthreads();                  // s_k holds this chunk
+            }
             // MFMA: the pass's factors' scores of columns [c0, c0 + CW) for the block's R tokens
 #pragma unroll
             for (int fi = 0; fi < NF; ++fi) {
@@ -82,10 +136,11 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
                     const int ct = cshare * CTW + j;
                     const int col = c0 + ct * 16;
                     if (col >= half) continue;            // wave-uniform: half % 16 == 0
-                    const bf16_t *krow = hkeys + (int64_t)(f * half + col + li) * dk;
+                    const bf16_t *krow = STAGE ? &s_k[fi][ct * 16 + li][kq * 8]
+                                               : hkeys + (int64_t)(f * half + col + li) * dk + kq * 8;
                     floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int s = 0; s < KS_MAX; ++s)
+                    for (int s = 0; s < KSM; ++s)
                         if (s < ks)
                             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                 qa[s], *reinterpret_cast<const bf16x8_t *>(krow + s * 32), acc, 0, 0, 0);
@@ -100,7 +155,7 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
                     }
                 }
             }
-            __syncthreads();
+            chunk_sync<WAVE_LOCAL>();
             // selection: lane g of a token folds K contiguous columns per factor into its lists
 #pragma unroll
             for (int sub = 0; sub < SUB; ++sub) {
@@ -116,8 +171,9 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
                 list_absorb<K>(ta, a);
                 if constexpr (PAIR) list_absorb<K>(tb, b);
             }
-            __syncthreads();
+            chunk_sync<WAVE_LOCAL>();
         }
+        __syncthreads();   // the lists overwrite the score chunks of every wavefront
         if constexpr (PAIR) {
             group_merge2<K, G>(ta, tb);
             const bool fa = stash_factor<K, G>(ta, kk, tie, g, s_idx[lr][0], s_val[lr][0]);
@@ -129,7 +185,7 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
             finite = finite && fa;
         }
     }
-    __syncthreads();
+    chunk_sync<WAVE_LOCAL>();
 
     uint64_t t[K];
     candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
@@ -146,9 +202,14 @@ static int launch_score_route(const void *q, const void *keys, int64_t N, int64_
     constexpr int R = 256 / G;
     const int64_t blocks = ceil_div(N, R) * H;
     if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: grid too large");
-    hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       static_cast<const bf16_t *>(q), static_cast<const bf16_t *>(keys), N, H, dk, half,
-                       width, tie, scores_out, index, weights);
+    const bf16_t *qq = static_cast<const bf16_t *>(q), *kk = static_cast<const bf16_t *>(keys);
+    constexpr bool STAGE = K <= 16;   // the larger lists need the LDS for themselves
+    if (dk <= 128)
+        hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR, 4, STAGE>), dim3((unsigned)blocks), dim3(256), 0,
+                           st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights);
+    else
+        hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR, KS_MAX, STAGE>), dim3((unsigned)blocks),
+                           dim3(256), 0, st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights);
     return check_launch("score_route_kernel");
 }
 

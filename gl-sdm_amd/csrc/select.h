@@ -2,7 +2,8 @@
 //
 // A group of G adjacent lanes owns one score row.  Each lane keeps a
 // descending top-K list of keys in registers (K a power of two).  Elements
-// arrive in chunks of K per lane: a chunk is sorted by a bitonic network and
+// arrive in chunks of K per lane: a chunk is sorted by a sorting network (the
+// 60-comparator network of sortnet16.h for K = 16, bitonic otherwise) and
 // merged into the list by a bitonic merge that keeps the K largest.  The G
 // lists are finally merged by a butterfly (DPP quad permutes for the two
 // innermost levels, __shfl_xor beyond), after which every lane of the group
@@ -21,6 +22,7 @@
 #pragma once
 
 #include "glsdm_internal.h"
+#include "sortnet16.h"
 
 namespace glsdm {
 
@@ -73,11 +75,26 @@ __device__ __forceinline__ void list_clear(uint64_t (&t)[K])
     for (int i = 0; i < K; ++i) t[i] = 0;
 }
 
+// Descending sort of 16 keys with the 60-comparator network (bitonic needs 80).
+__device__ __forceinline__ void sort16_desc(uint64_t (&v)[16])
+{
+#pragma unroll
+    for (int c = 0; c < SORTNET16_SIZE; ++c) {
+        const int i = SORTNET16[c][0], j = SORTNET16[c][1];
+        const uint64_t a = v[i], b = v[j];
+        v[i] = a > b ? a : b;
+        v[j] = a > b ? b : a;
+    }
+}
+
 // Merge one unsorted chunk of K keys into the lane's running list.
 template <int K>
 __device__ __forceinline__ void list_absorb(uint64_t (&t)[K], uint64_t (&c)[K])
 {
-    bitonic_sort<K, true>(c);
+    if constexpr (K == 16)
+        sort16_desc(c);
+    else
+        bitonic_sort<K, true>(c);
     merge_top<K>(t, c);
 }
 
