@@ -89,9 +89,8 @@ class Pipeline:
         self.out = torch.empty(B, C, H, D, dtype=torch.float32, device=device)
         self.rows = B * H * half * half
         self.E = B * C * H * k
-        self.key_bits = (self.rows * C - 1).bit_length()
         size = ctypes.c_size_t(0)
-        N.call("glsdm_commit_workspace_bytes", self.E, self.key_bits, ctypes.byref(size))
+        N.call("glsdm_commit_workspace_bytes", self.E, self.rows, ctypes.byref(size))
         self.ws = torch.empty(size.value, dtype=torch.uint8, device=device)
         self.unique = torch.zeros(1, dtype=torch.int64, device=device)
         self.mem_stream = torch.cuda.current_stream(device)
@@ -133,7 +132,7 @@ class Pipeline:
             p(self.out), N.F32, st))
         self._timed("commit", stream, lambda: N.call(
             "glsdm_commit", p(self.bank), N.BF16, self.rows, D, p(self.addr[e]), p(self.delta[e]), N.BF16,
-            p(self.ckeys[e]), 0, self.key_bits, self.E, p(self.ws), self.ws.numel(),
+            p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(),
             p(self.unique) if count_unique else None, st))
 
     def step_serial(self):

@@ -9,22 +9,31 @@
 // Pipeline (stream-ordered, no host sync, 3 + passes launches):
 //   1. prep:      zero the per-pass digit histograms, look-back words and tile
 //                 counters of the workspace (a fill kernel, safe under capture).
-//   2. pack+hist: v[e] = (key[e] - key_min) << ebits | e, ebits = bits of E-1,
-//                 and the digit histograms of every radix pass in one read.
-//                 Ordering the packed words orders by (key, entry): a stable
-//                 key sort, with the entry id riding along for free.
-//   3. passes:    LSD radix sort over bits [ebits, ebits + key_bits), 8-bit
+//   2. pack+hist: v[e] = a(e) << ebits | e with a(e) the row address (rows for an
+//                 out-of-range address) and ebits = bits of E-1, plus the digit
+//                 histograms of every radix pass in one read.
+//   3. passes:    LSD radix sort of the packed words over the address bits, 8-bit
 //                 digits, one kernel per pass: tiles take ids in launch order,
 //                 rank their items stably (wavefront ballots: match-any over the
 //                 8 digit bits, per-wave LDS counters), publish per-digit counts
 //                 and resolve their global offsets by decoupled look-back over
 //                 earlier tiles' published counts.  The entry bits below ebits
-//                 are never sorted: they start ascending and every pass is stable.
-//   4. segment:   a wavefront per 64 sorted positions loads entry ids and
-//                 addresses in parallel, finds run heads with a ballot, and its
-//                 lane groups each walk one run in order, summing the deltas in
-//                 fp32 registers, then read-modify-write that bank row once.
-//                 Exactly one lane group writes each touched row.
+//                 are never sorted: they start ascending and every pass is
+//                 stable, so each address's entries end up in arrival order.
+//   4. segment:   a wavefront per 64 sorted positions reads the addresses from
+//                 the sorted words, finds run heads with a ballot, and its lane
+//                 groups each walk one run, summing the deltas in fp32 registers
+//                 in (key, entry) order, then read-modify-write that bank row
+//                 once.  Exactly one lane group writes each touched row.
+//                 A run's arrival order already is its key order when its keys
+//                 rise with the entry index (one proposal: keys grow with the
+//                 token position); this is checked while walking, and a run
+//                 that is not in key order is summed in (key, entry) order by a
+//                 selection loop over the run instead.
+// Grouping by address and ordering each address's deltas by (key, entry) is
+// the reference's stable key sort followed by grouping of equal consecutive
+// addresses whenever its keys keep equal addresses together (keys = addresses,
+// and the stack's addr*(C*L) + pos*L + layer).
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -100,8 +109,7 @@ __global__ __launch_bounds__(256) void commit_prep_kernel(uint32_t *__restrict__
     if (tid < MAX_PASSES + 1) counter[tid] = 0;
 }
 
-__global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ keys,
-                                                        const int64_t *__restrict__ addresses, int64_t key_min,
+__global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ addresses, int64_t rows,
                                                         int ebits, int passes, int64_t n,
                                                         uint64_t *__restrict__ out, uint32_t *__restrict__ ghist)
 {
@@ -110,8 +118,9 @@ __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restric
     __syncthreads();
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t k = (keys ? keys[i] : addresses[i]) - key_min;
-        const uint64_t v = ((uint64_t)k << ebits) | (uint64_t)i;
+        const int64_t a = addresses[i];
+        const uint64_t row = (a >= 0 && a < rows) ? (uint64_t)a : (uint64_t)rows;   // out of range: one run, dropped
+        const uint64_t v = (row << ebits) | (uint64_t)i;
         out[i] = v;
         for (int p = 0; p < passes; ++p)
             atomicAdd(&h[p][(uint32_t)(v >> (ebits + p * RADIX_BITS)) & (RADIX - 1)], 1u);
@@ -223,89 +232,100 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
 // (one bank row each) walk the address runs that start in the wave's window.
 template <typename TB, typename TD, int VEC, int CH>
 __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int64_t rows, int64_t D,
-                                                      const int64_t *__restrict__ addresses,
+                                                      const int64_t *__restrict__ keys,
                                                       const TD *__restrict__ deltas,
-                                                      const uint64_t *__restrict__ sorted, int64_t n,
-                                                      uint64_t emask, int nv, int lpr,
-                                                      unsigned long long *__restrict__ unique_out)
+                                                      const uint64_t *__restrict__ sorted, int64_t n, int ebits,
+                                                      int nv, int lpr, unsigned long long *__restrict__ unique_out)
 {
-    __shared__ int64_t s_e[4][64];
-    __shared__ int64_t s_a[4][64];
+    __shared__ uint64_t s_w[4][64];
     __shared__ int s_head[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
     const int64_t p = p0 + lane;
     const bool valid = p < n;
-    // entry id and address of this position (-1 for padding or a corrupt id)
-    int64_t e = valid ? (int64_t)(sorted[p] & emask) : n;
-    const int64_t a = e < n ? addresses[e] : -1;
+    const uint64_t emask = (1ull << ebits) - 1ull;
+    const uint64_t w = valid ? sorted[p] : ~0ull;
+    const int64_t a = valid ? (int64_t)(w >> ebits) : -1;
     int64_t prev = __shfl_up(a, 1);
-    if (lane == 0) {
-        prev = -2;
-        if (p0 > 0 && p0 - 1 < n) {
-            const int64_t ep = (int64_t)(sorted[p0 - 1] & emask);
-            prev = ep < n ? addresses[ep] : -1;
-        }
-    }
+    if (lane == 0) prev = (p0 > 0 && p0 - 1 < n) ? (int64_t)(sorted[p0 - 1] >> ebits) : -2;
     const bool head = valid && a != prev;
     const uint64_t heads = __ballot(head);
-    s_e[wave][lane] = e;
-    s_a[wave][lane] = a;
+    s_w[wave][lane] = w;
     if (head) s_head[wave][__popcll(heads & ((1ull << lane) - 1ull))] = lane;
     const int nheads = __popcll(heads);
     // rows this window will write: heads whose address is in range (one atomic per wave)
-    const uint64_t live = __ballot(head && a >= 0 && a < rows);
+    const uint64_t live = __ballot(head && a < rows);
     if (unique_out && lane == 0 && live) atomicAdd(unique_out, (unsigned long long)__popcll(live));
     __syncthreads();
 
     const int ng = 64 / lpr;
     const int grp = lane / lpr, li = lane % lpr;
+    auto word_at = [&](int q) -> uint64_t { return q < 64 ? s_w[wave][q] : sorted[p0 + q]; };
+    auto add_delta = [&](int64_t ent, float (&acc)[CH][VEC]) {
+        if (ent >= n) return;                           // impossible after a correct sort; never read out of bounds
+        const TD *src = deltas + ent * D;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+            if (v < nv) {
+                float x[VEC];
+                VecLoad<TD, VEC>::load(src + (int64_t)v * VEC, x);
+#pragma unroll
+                for (int y = 0; y < VEC; ++y) acc[c][y] += x[y];
+            }
+        }
+    };
     for (int r = grp; r < nheads; r += ng) {
         const int h = s_head[wave][r];
-        const int64_t row_addr = s_a[wave][h];
-        const bool in_range = row_addr >= 0 && row_addr < rows;
-        TB *row = bank + (in_range ? row_addr : 0) * D;
+        const uint64_t hw = s_w[wave][h];
+        const int64_t row_addr = (int64_t)(hw >> ebits);
+        if (row_addr >= rows) continue;                 // out-of-range entries: dropped
+        // run length: positions after the head with the same address
+        int len = 1;
+        while (p0 + h + len < n && (int64_t)(word_at(h + len) >> ebits) == row_addr) ++len;
+        TB *row = bank + row_addr * D;
         float old[CH][VEC], acc[CH][VEC];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
 #pragma unroll
-            for (int x = 0; x < VEC; ++x) acc[c][x] = 0.0f;
-            if (in_range && v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
+            for (int x = 0; x < VEC; ++x) acc[c][x] = 0.0f;     // sums start from +0
+            if (v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
         }
-        int q = h;
-        for (;;) {
-            int64_t ent;
-            if (q < 64) {
-                ent = s_e[wave][q];
-            } else {
-                ent = (int64_t)(sorted[p0 + q] & emask);
+        // arrival order is key order unless a later entry has a smaller key
+        bool in_order = true;
+        auto key_of = [&](uint64_t word) -> int64_t {
+            const int64_t e = (int64_t)(word & emask);
+            return e < n ? keys[e] : INT64_MAX;
+        };
+        if (keys && len > 1) {
+            int64_t k0 = key_of(hw);
+            for (int q = 1; q < len && in_order; ++q) {
+                const int64_t k1 = key_of(word_at(h + q));
+                in_order = k1 >= k0;
+                k0 = k1;
             }
-            if (in_range && ent < n) {
-                const TD *src = deltas + ent * D;
-#pragma unroll
-                for (int c = 0; c < CH; ++c) {
-                    const int v = li + c * lpr;
-                    if (v < nv) {
-                        float x[VEC];
-                        VecLoad<TD, VEC>::load(src + (int64_t)v * VEC, x);
-#pragma unroll
-                        for (int y = 0; y < VEC; ++y) acc[c][y] += x[y];
-                    }
+        }
+        if (in_order) {
+            for (int q = 0; q < len; ++q) add_delta((int64_t)(word_at(h + q) & emask), acc);
+        } else {
+            // exact (key, entry) order by repeated selection of the next smallest pair
+            int64_t last_k = INT64_MIN, last_e = -1;
+            for (int r2 = 0; r2 < len; ++r2) {
+                int64_t best_k = INT64_MAX, best_e = INT64_MAX;
+                for (int q = 0; q < len; ++q) {
+                    const uint64_t wq = word_at(h + q);
+                    const int64_t e = (int64_t)(wq & emask);
+                    const int64_t k = key_of(wq);
+                    const bool after = k > last_k || (k == last_k && e > last_e);
+                    const bool before = k < best_k || (k == best_k && e < best_e);
+                    if (after && before) { best_k = k; best_e = e; }
                 }
+                add_delta(best_e, acc);
+                last_k = best_k;
+                last_e = best_e;
             }
-            ++q;
-            if (p0 + q >= n) break;
-            int64_t next;
-            if (q < 64) {
-                next = s_a[wave][q];
-            } else {
-                const int64_t en = (int64_t)(sorted[p0 + q] & emask);
-                next = en < n ? addresses[en] : -1;
-            }
-            if (next != row_addr) break;
         }
-        if (!in_range) continue;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
@@ -319,8 +339,8 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
 }
 
 template <typename TB, typename TD, int VEC>
-static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t *addresses,
-                             const void *deltas, const uint64_t *sorted, int64_t n, uint64_t emask,
+static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t *keys,
+                             const void *deltas, const uint64_t *sorted, int64_t n, int ebits,
                              const RowPlan &p, int64_t *unique_out, hipStream_t st)
 {
     const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
@@ -328,18 +348,18 @@ static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t 
     const TD *dl = static_cast<const TD *>(deltas);
     auto *u = reinterpret_cast<unsigned long long *>(unique_out);
     switch (p.ch) {
-    case 1: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 1>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
-    case 2: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 2>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
+    case 1: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 1>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
+    case 2: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 2>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
     case 3:
-    case 4: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 4>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
-    default: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 8>), grid, block, 0, st, bk, rows, D, addresses, dl, sorted, n, emask, p.nv, p.lpr, u); break;
+    case 4: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 4>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
+    default: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 8>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
     }
     return check_launch("segment_kernel");
 }
 
 template <typename TB, typename TD>
-static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *addresses,
-                            const void *deltas, const uint64_t *sorted, int64_t n, uint64_t emask,
+static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys,
+                            const void *deltas, const uint64_t *sorted, int64_t n, int ebits,
                             int64_t *unique_out, hipStream_t st)
 {
     // One vector width for both operands: the wider type's 16-byte vector.
@@ -349,44 +369,51 @@ static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *
         RowPlan p{VEC, (int)(D / VEC), 0, 0};
         p.lpr = pow2_ceil(p.nv) < 64 ? pow2_ceil(p.nv) : 64;
         p.ch = (int)ceil_div(p.nv, p.lpr);
-        return launch_segment_ch<TB, TD, VEC>(bank, rows, D, addresses, deltas, sorted, n, emask, p, unique_out, st);
+        return launch_segment_ch<TB, TD, VEC>(bank, rows, D, keys, deltas, sorted, n, ebits, p, unique_out, st);
     }
     RowPlan p{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
-    return launch_segment_ch<TB, TD, 1>(bank, rows, D, addresses, deltas, sorted, n, emask, p, unique_out, st);
+    return launch_segment_ch<TB, TD, 1>(bank, rows, D, keys, deltas, sorted, n, ebits, p, unique_out, st);
 }
 
 }  // namespace glsdm
 
 using namespace glsdm;
 
-extern "C" int glsdm_commit_workspace_bytes(int64_t entries, int32_t key_bits, size_t *bytes)
+static int address_bits(int64_t rows)
+{
+    int b = 0;                         // bits for the values 0 .. rows (rows = "out of range")
+    while (((int64_t)1 << b) <= rows) ++b;
+    return b;
+}
+
+extern "C" int glsdm_commit_workspace_bytes(int64_t entries, int64_t rows, size_t *bytes)
 {
     if (!bytes) return fail(GLSDM_ERR_ARG, "commit_workspace_bytes: null output");
-    if (entries < 0 || key_bits < 0 || key_bits > 63) return fail(GLSDM_ERR_ARG, "commit_workspace_bytes: bad arguments");
+    if (entries < 0 || rows < 1) return fail(GLSDM_ERR_ARG, "commit_workspace_bytes: bad arguments");
     if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "commit: more than 2^30 entries");
-    if (entries > 0 && key_bits + entry_bits(entries) > 64)
-        return fail(GLSDM_ERR_UNSUPPORTED, "commit: key_bits %d + entry bits %d exceed 64", key_bits, entry_bits(entries));
-    *bytes = entries == 0 ? 0 : plan_workspace(nullptr, entries, pass_count(key_bits)).bytes;
+    if (entries > 0 && address_bits(rows) + entry_bits(entries) > 64)
+        return fail(GLSDM_ERR_UNSUPPORTED, "commit: address bits %d + entry bits %d exceed 64", address_bits(rows),
+                    entry_bits(entries));
+    *bytes = entries == 0 ? 0 : plan_workspace(nullptr, entries, pass_count(address_bits(rows))).bytes;
     return GLSDM_OK;
 }
 
 extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
                             const int64_t *addresses, const void *deltas, int32_t delta_dtype,
-                            const int64_t *keys, int64_t key_min, int32_t key_bits, int64_t entries,
-                            void *workspace, size_t workspace_bytes, int64_t *unique_out, void *stream)
+                            const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
+                            int64_t *unique_out, void *stream)
 {
     if (rows < 1 || D < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit: bad shape rows=%lld D=%lld entries=%lld", (long long)rows, (long long)D, (long long)entries);
     if (!dtype_ok(bank_dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "commit: bad dtype");
-    if (key_bits < 0 || key_bits > 63) return fail(GLSDM_ERR_ARG, "commit: key_bits must be in [0, 63]");
     if (entries == 0) return GLSDM_OK;
     if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "commit: more than 2^30 entries");
     if (!bank || !addresses || !deltas) return fail(GLSDM_ERR_ARG, "commit: null pointer");
     if (D > 512 && D % 8 != 0) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld not a multiple of 8 above 512", (long long)D);
     if (D > 64 * 8 * 4) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld above 2048", (long long)D);
-    const int ebits = entry_bits(entries);
-    if (key_bits + ebits > 64)
-        return fail(GLSDM_ERR_UNSUPPORTED, "commit: key_bits %d + entry bits %d exceed 64", key_bits, ebits);
-    const int passes = pass_count(key_bits);
+    const int ebits = entry_bits(entries), abits = address_bits(rows);
+    if (abits + ebits > 64)
+        return fail(GLSDM_ERR_UNSUPPORTED, "commit: address bits %d + entry bits %d exceed 64", abits, ebits);
+    const int passes = pass_count(abits);
     CommitWorkspace ws = plan_workspace(workspace, entries, passes);
     if (!workspace || workspace_bytes < ws.bytes)
         return fail(GLSDM_ERR_WORKSPACE, "commit: workspace of %zu bytes needed, %zu given", ws.bytes, workspace_bytes);
@@ -397,8 +424,8 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
     hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
                        (int64_t)ws.status_words, ws.counter);
     const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), GLSDM_PACK_BLOCKS);
-    hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, keys, addresses, key_min, ebits,
-                       passes, entries, ws.a, ws.ghist);
+    hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, passes,
+                       entries, ws.a, ws.ghist);
     int rc = check_launch("commit pack");
     if (rc) return rc;
 
@@ -411,12 +438,11 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
         uint64_t *t = src; src = dst; dst = t;
     }
 
-    const uint64_t emask = (1ull << ebits) - 1ull;
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
-        return launch_segment_t<float, float>(bank, rows, D, addresses, deltas, src, entries, emask, unique_out, st);
+        return launch_segment_t<float, float>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
-        return launch_segment_t<float, bf16_t>(bank, rows, D, addresses, deltas, src, entries, emask, unique_out, st);
+        return launch_segment_t<float, bf16_t>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
     if (bank_dtype == GLSDM_BF16 && delta_dtype == GLSDM_F32)
-        return launch_segment_t<bf16_t, float>(bank, rows, D, addresses, deltas, src, entries, emask, unique_out, st);
-    return launch_segment_t<bf16_t, bf16_t>(bank, rows, D, addresses, deltas, src, entries, emask, unique_out, st);
+        return launch_segment_t<bf16_t, float>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
+    return launch_segment_t<bf16_t, bf16_t>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
 }

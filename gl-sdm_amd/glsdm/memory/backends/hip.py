@@ -178,18 +178,13 @@ def gather_rows(values, index):
     return out
 
 
-def _bits(n):
-    """Bits needed for the values 0 .. n-1."""
-    return max(int(n - 1).bit_length(), 0)
-
-
-def commit_workspace_bytes(entries, key_bits):
+def commit_workspace_bytes(entries, rows):
     size = N.ctypes.c_size_t(0)
-    N.call("glsdm_commit_workspace_bytes", entries, key_bits, N.ctypes.byref(size))
+    N.call("glsdm_commit_workspace_bytes", entries, rows, N.ctypes.byref(size))
     return size.value
 
 
-def commit(memory, indices, deltas, keys=None, donate=False, key_bound=None, workspace=None, unique=None):
+def commit(memory, indices, deltas, keys=None, donate=False, workspace=None, unique=None):
     """Deterministic commit of ``deltas [E, D]`` at absolute rows ``indices [E]``.
 
     ``memory`` is any contiguous tensor whose last dimension is D (e.g. the
@@ -197,9 +192,8 @@ def commit(memory, indices, deltas, keys=None, donate=False, key_bound=None, wor
     ``memory`` itself updated in place when ``donate=True`` (the caller gives
     up the old contents; no full-bank copy is made).
 
-    ``keys`` (int64 [E], default: the addresses) orders colliding deltas.
-    ``key_bound`` is an exclusive upper bound of the keys (all keys >= 0); when
-    omitted it is read from the keys with one device-to-host copy.
+    ``keys`` (int64 [E], default: arrival order) orders colliding deltas: each
+    address's deltas are summed from +0 in ascending (key, entry) order.
     ``workspace`` (uint8 device tensor) and ``unique`` (int64 [1] device
     counter, incremented by the number of touched rows) are optional.
     """
@@ -216,18 +210,10 @@ def commit(memory, indices, deltas, keys=None, donate=False, key_bound=None, wor
     if E == 0:
         return out
     rows = memory.numel() // D
-    key_min = 0
-    if keys is None:
-        key_bits = _bits(rows)
-    elif key_bound is not None:
-        key_bits = _bits(int(key_bound))
-    else:
-        lo, hi = (int(v) for v in torch.aminmax(keys))
-        key_min, key_bits = lo, _bits(hi - lo + 1)
-    need = commit_workspace_bytes(E, key_bits)
+    need = commit_workspace_bytes(E, rows)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=device)
     N.call("glsdm_commit", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(deltas),
-           N.dtype_code(deltas), N.ptr(keys), key_min, key_bits, E, N.ptr(workspace), workspace.numel(),
-           N.ptr(unique), N.stream(device))
+           N.dtype_code(deltas), N.ptr(keys), E, N.ptr(workspace), workspace.numel(), N.ptr(unique),
+           N.stream(device))
     return out

@@ -32,7 +32,6 @@ class WriteProposal:
     deltas: torch.Tensor     # [E, value_dim], already weighted (fp32 or bf16)
     lineage: object
     sort_keys: torch.Tensor | None = None  # optional address/token/depth order, int64 [E]
-    key_bound: int | None = None           # exclusive bound of sort_keys (saves a device read)
 
 
 @dataclass(frozen=True)

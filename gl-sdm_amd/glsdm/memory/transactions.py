@@ -46,11 +46,9 @@ def commit(view, buffer, reference=False, backend="hip", donate=False):
     if len({d.dtype for d in deltas}) > 1:
         deltas = [d.float() for d in deltas]
     delta = _cat(deltas)
-    keys, bound = None, None
-    if all(keyed):
-        keys = _cat([p.sort_keys.reshape(-1) for p in props])
-        bounds = [p.key_bound for p in props]
-        bound = max(bounds) if all(b is not None for b in bounds) else None
+    # unkeyed proposals collide in arrival order: the reference sorts them by address
+    # with a stable sort, which keeps arrival order within an address
+    keys = _cat([p.sort_keys.reshape(-1) for p in props]) if all(keyed) else None
     updated = hip.commit(view.values, idx.contiguous(), delta.contiguous(),
-                         None if keys is None else keys.contiguous(), donate=donate, key_bound=bound)
+                         None if keys is None else keys.contiguous(), donate=donate)
     return MemoryView(updated, view.version + 1, view.lineage)

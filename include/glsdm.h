@@ -117,35 +117,35 @@ int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64
                       int64_t *index, float *weights, void *stream);
 
 /*
- * Bytes of workspace glsdm_commit needs for `entries` deltas whose keys span
- * `key_bits` bits (keys - key_min < 2^key_bits).
+ * Bytes of workspace glsdm_commit needs for `entries` deltas into a bank of
+ * `rows` rows.
  */
-int glsdm_commit_workspace_bytes(int64_t entries, int32_t key_bits, size_t *bytes);
+int glsdm_commit_workspace_bytes(int64_t entries, int64_t rows, size_t *bytes);
 
 /*
  * Deterministic buffered commit, in place on `bank`.
  *   bank      [rows, D] of bank_dtype, updated in place
- *   addresses [entries] int64 absolute rows
+ *   addresses [entries] int64 absolute rows; entries outside [0, rows) are dropped
  *   deltas    [entries, D] of delta_dtype
- *   keys      [entries] int64 collision order, or NULL for keys = addresses;
- *             keys must place equal addresses next to each other once sorted
- *             (true for keys = addresses and for address-major keys such as
- *             addr*(C*L) + pos*L + layer)
- *   key_min, key_bits: every key k satisfies 0 <= k - key_min < 2^key_bits
+ *   keys      [entries] int64 collision order, or NULL for arrival order
  *   unique_out: optional int64 device counter; the number of touched rows is
  *             added to it (NULL to skip)
  * Result: for every address a, bank[a] = round(bank[a] + s_a) where s_a is the
- * fp32 sum, starting from 0, of a's deltas in stable ascending key order;
- * round is identity for fp32 and round-to-nearest-even for bf16.  No floating
- * point atomics: the result is bitwise reproducible.
+ * fp32 sum, starting from +0, of a's deltas in ascending (key, entry index)
+ * order; round is identity for fp32 and round-to-nearest-even for bf16.  This
+ * equals the reference's stable key sort followed by grouping of equal
+ * consecutive addresses whenever the keys keep equal addresses together (keys =
+ * addresses, or the stack's addr*(C*L) + pos*L + layer).  No floating point
+ * atomics: the result is bitwise reproducible.  The keys are only read for
+ * addresses with several entries.
  * Replaces: S/memory/transactions.py:69-97 (commit; torch branch order) and
  * S/memory/backends/commit.py:36-58 (_Commit.forward), without the full-bank
  * clone (callers that need the old bank copy it first).
  */
 int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
                  const int64_t *addresses, const void *deltas, int32_t delta_dtype,
-                 const int64_t *keys, int64_t key_min, int32_t key_bits, int64_t entries,
-                 void *workspace, size_t workspace_bytes, int64_t *unique_out, void *stream);
+                 const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
+                 int64_t *unique_out, void *stream);
 
 /*
  * Absolute addresses (b*H + h)*S + index[b,t,h,j] for index [B,T,H,width].

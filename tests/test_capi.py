@@ -43,12 +43,13 @@ def test_route_rejects_bad_arguments_before_launch():
 
 def test_commit_workspace_contract():
     size = ctypes.c_size_t(0)
-    assert _rc("glsdm_commit_workspace_bytes", 524288, 31, ctypes.byref(size)) == N.OK
+    assert _rc("glsdm_commit_workspace_bytes", 524288, 1 << 22, ctypes.byref(size)) == N.OK
     assert size.value >= 2 * 8 * 524288
-    assert _rc("glsdm_commit_workspace_bytes", 1 << 40, 40, ctypes.byref(size)) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_commit_workspace_bytes", 1 << 31, 16, ctypes.byref(size)) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_commit_workspace_bytes", 1 << 29, 1 << 40, ctypes.byref(size)) == N.ERR_UNSUPPORTED
     assert _rc("glsdm_commit", ctypes.c_void_p(1), 0, 16, 4, ctypes.c_void_p(1), ctypes.c_void_p(1), 0,
-               None, 0, 4, 8, None, 0, None, None) == N.ERR_WORKSPACE
-    assert _rc("glsdm_commit", None, 0, 16, 4, None, None, 0, None, 0, 4, 0, None, 0, None, None) == N.OK
+               None, 8, None, 0, None, None) == N.ERR_WORKSPACE
+    assert _rc("glsdm_commit", None, 0, 16, 4, None, None, 0, None, 0, None, 0, None, None) == N.OK
 
 
 def test_read_and_score_envelopes():

@@ -91,16 +91,32 @@ def test_commit_donate_repeat_and_untouched(device):
     assert torch.equal(first.cpu()[untouched], flat[untouched])
 
 
-def test_commit_key_bound_and_offset_keys(device):
+def test_commit_negative_and_interleaved_keys(device):
     flat, addr, delta, _ = _case(700, 16, 5000, 700, seed=8)
-    keys = addr * 5000 + torch.arange(5000) - 12345          # negative keys: offset by their minimum
+    keys = addr * 5000 + torch.arange(5000) - 12345          # negative keys are ordinary int64 keys
     out = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
     ref, _ = c_oracle.commit(flat, addr, delta, keys)
     assert torch.equal(out.cpu(), ref)
-    pos = addr * 5000 + torch.arange(5000)
-    out2 = hip.commit(flat.to(device), addr.to(device), delta.to(device), pos.to(device), key_bound=700 * 5000)
-    ref2, _ = c_oracle.commit(flat, addr, delta, pos)
+    # two proposals (layers) concatenated: within an address the key order interleaves them
+    pos = torch.randint(0, 512, (5000,))
+    layer = (torch.arange(5000) >= 2500).long()
+    keys2 = addr * (512 * 2) + pos * 2 + layer
+    out2 = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys2.to(device))
+    ref2, _ = c_oracle.commit(flat, addr, delta, keys2)
     assert torch.equal(out2.cpu(), ref2)
+
+
+def test_commit_long_unordered_run(device):
+    """One hot row with 3000 deltas in scrambled key order (a skewed, multi-layer commit)."""
+    g = torch.Generator().manual_seed(12)
+    flat = torch.randn(64, 32, generator=g)
+    addr = torch.full((3000,), 17)
+    addr[::7] = torch.randint(0, 64, (429,), generator=g)
+    delta = torch.randn(3000, 32, generator=g) * 0.5
+    keys = addr * 100000 + torch.randperm(3000, generator=g)
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
+    ref, _ = c_oracle.commit(flat, addr, delta, keys)
+    assert torch.equal(out.cpu(), ref)
 
 
 def test_commit_drops_out_of_range_addresses(device):

@@ -48,7 +48,7 @@ def test_config1_pipeline(device):
     assert torch.equal(widx.cpu(), ridx)
     addr, keys = hip.proposal_keys(view.values, widx, 0, 512, 1, 0)
     p = WriteProposal(view.version, addr.reshape(-1), c["delta"].reshape(-1, c["D"]).to(device), view.lineage,
-                      keys.reshape(-1), key_bound=values.shape[0] * values.shape[1] * values.shape[2] * 512)
+                      keys.reshape(-1))
     new = commit(view, merge(view, [p]))
     raddr = torch_oracle.absolute_addresses(values, ridx).reshape(-1)
     rkeys = raddr * 512 + torch.arange(512).view(1, 512, 1, 1).expand(2, 512, 1, 8).reshape(-1)

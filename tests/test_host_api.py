@@ -91,4 +91,3 @@ def test_route_size_validation():
     with pytest.raises(ValueError):
         hip._square_root(15)
     assert hip._square_root(65536) == 256
-    assert hip._bits(1) == 0 and hip._bits(2) == 1 and hip._bits(4194304) == 22
