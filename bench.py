@@ -31,7 +31,15 @@ sys.path.insert(0, os.path.join(ROOT, "gl-sdm_amd"))
 HBM_PEAK = 8.0e12          # B/s, MI355X
 MFMA_BF16_PEAK = 2.5e15    # FLOP/s dense bf16
 
-CFG = dict(B=8, T=2048, C=512, H=8, half=256, dk=128, D=128, k=16)
+CONFIGS = {
+    # the reference's CPU-runnable case (fp32, one epoch)
+    1: dict(B=2, T=512, C=512, H=1, half=64, dk=64, D=256, k=8, dtype=torch.float32, skew=False),
+    # the headline roofline config
+    2: dict(B=8, T=2048, C=512, H=8, half=256, dk=128, D=128, k=16, dtype=torch.bfloat16, skew=False),
+    # 2^20-slot bank, Zipf(1.1)-skewed routes over 4096 product clusters
+    3: dict(B=4, T=4096, C=512, H=1, half=1024, dk=128, D=512, k=32, dtype=torch.bfloat16, skew=True),
+}
+CFG = CONFIGS[2]
 
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this
 # workload, scaled by a 256 MiB copy measured in the same run (FETCH x 1.9998,
@@ -45,31 +53,53 @@ TRAFFIC_PER_LAUNCH = {
 }
 
 
+def _zipf_queries(g, B, T, H, centres, dk, s=1.1):
+    """Queries around product cluster z = (z0, z1) with z ~ Zipf(s) over a seeded rank permutation."""
+    n = centres[0].shape[0]
+    p = torch.arange(1, n * n + 1, dtype=torch.float64).pow(-s)
+    perm = torch.randperm(n * n, generator=g)
+    z = perm[torch.multinomial(p / p.sum(), B * T * H, replacement=True, generator=g)]
+    q = centres[0][z // n] + centres[1][z % n] + 0.05 * torch.randn(B * T * H, dk, generator=g)
+    return torch.nn.functional.normalize(q, dim=-1).view(B, T, H, dk)
+
+
 def make_inputs(cfg, seed=0):
-    """Seeded CPU generation in a fixed order, then bf16 (config-2 protocol)."""
+    """Seeded CPU generation in a fixed order, then the config's dtype."""
     g = torch.Generator("cpu").manual_seed(seed)
     B, T, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "H", "half", "dk", "D", "k"))
+    dt = cfg["dtype"]
     norm = torch.nn.functional.normalize
-    keys = norm(torch.randn(H, 2 * half, dk, generator=g), dim=-1).bfloat16()
-    bank = (torch.randn(H, half * half, D, generator=g) * 0.02).bfloat16()
-    qr = norm(torch.randn(B, T, H, dk, generator=g), dim=-1).bfloat16()
-    qw = norm(torch.randn(B, T, H, dk, generator=g), dim=-1).bfloat16()
-    delta = (torch.randn(B, T, H, k, D, generator=g) * 0.02).bfloat16()
-    return keys, bank, qr, qw, delta
+    if cfg["skew"]:
+        centres = [norm(torch.randn(64, dk, generator=g), dim=-1) for _ in range(2)]
+        sub = [norm(centres[f][torch.arange(half) % 64] + 0.05 * torch.randn(half, dk, generator=g), dim=-1)
+               for f in range(2)]
+        keys = torch.cat(sub).view(1, 2 * half, dk).expand(H, -1, -1).contiguous()
+    else:
+        keys = norm(torch.randn(H, 2 * half, dk, generator=g), dim=-1)
+    bank = (torch.randn(H, half * half, D, generator=g) * 0.02).to(dt)
+    if cfg["skew"]:
+        qr = _zipf_queries(g, B, T, H, centres, dk)
+        qw = _zipf_queries(g, B, T, H, centres, dk)
+    else:
+        qr = norm(torch.randn(B, T, H, dk, generator=g), dim=-1)
+        qw = norm(torch.randn(B, T, H, dk, generator=g), dim=-1)
+    delta = (torch.randn(B, T, H, k, D, generator=g) * 0.02).to(dt)
+    return keys.bfloat16(), bank, qr.bfloat16(), qw.bfloat16(), delta
 
 
 class Pipeline:
     """Preallocated buffers and direct C-ABI calls for the 4-epoch workload.
 
     Two schedules of the same work:
-    * serial (--schedule serial): every call on one stream, epoch after epoch;
-    * overlapped (the timed default): scoring+routing never reads the bank, so
+    * serial (the timed default): every call on one stream, epoch after epoch;
+    * overlapped (--schedule overlap): scoring+routing never reads the bank, so
       the route stream computes epoch e+1's read and write routes and proposal
       keys while the memory stream runs epoch e's read and commit.  The memory
       stream waits for an epoch's routes with an event; read(e+1) follows
       commit(e) in stream order, so every read still sees the bank version of
       its epoch.  Measured on MI355X it gains ~2%: the concurrent kernels slow
-      each other down by almost as much as they overlap.
+      each other down by almost as much as they overlap (and their individual
+      durations stop being a clean roofline measurement), so it is not the default.
     """
 
     def __init__(self, cfg, device):
@@ -127,11 +157,12 @@ class Pipeline:
     def memory(self, e, stream, count_unique=False):
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, D, k = (c[x] for x in ("B", "C", "H", "half", "D", "k"))
+        dt = N.dtype_code(self.bank)
         self._timed("read", stream, lambda: N.call(
-            "glsdm_read", p(self.bank), N.BF16, B, H, half * half, D, C, k, p(self.idx[e]), p(self.w[e]),
+            "glsdm_read", p(self.bank), dt, B, H, half * half, D, C, k, p(self.idx[e]), p(self.w[e]),
             p(self.out), N.F32, st))
         self._timed("commit", stream, lambda: N.call(
-            "glsdm_commit", p(self.bank), N.BF16, self.rows, D, p(self.addr[e]), p(self.delta[e]), N.BF16,
+            "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.delta[e]), dt,
             p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(),
             p(self.unique) if count_unique else None, st))
 
@@ -167,13 +198,14 @@ class Pipeline:
 
 
 def algorithmic_bytes(cfg, unique):
-    """Read + commit HBM bytes per epoch (bf16 bank/queries/deltas)."""
+    """Read + commit HBM bytes per epoch (queries bf16; bank and deltas in the config's dtype)."""
     B, C, H, dk, D, k = (cfg[x] for x in ("B", "C", "H", "dk", "D", "k"))
+    sv = torch.tensor([], dtype=cfg["dtype"]).element_size()
     rows = B * C * H
-    read_kernel = rows * (k * D * 2 + D * 4 + k * 12)            # gathers + fp32 out + idx/w
+    read_kernel = rows * (k * D * sv + D * 4 + k * 12)           # gathers + fp32 out + idx/w
     read = read_kernel + rows * dk * 2                            # + queries read once
     E = rows * k
-    commit = [E * D * 2 + E * 16 + 2 * u * D * 2 for u in unique]
+    commit = [E * D * sv + E * 16 + 2 * u * D * sv for u in unique]
     return read, read_kernel, commit
 
 
@@ -184,7 +216,7 @@ def cpu_baseline(cfg, budget_s=12.0):
     keys, bank, qr, qw, delta = make_inputs(cfg)
     C, H, half, D, k = (cfg[x] for x in ("C", "H", "half", "D", "k"))
     S = half * half
-    bank0 = bank.float().reshape(1, H, S, D)
+    bank0 = bank.float().reshape(1, H, S, D)   # request 0's replica
     flat = bank0.reshape(-1, D).clone()
     tokens, t0, e = 0, time.perf_counter(), 0
     while True:
@@ -206,7 +238,7 @@ def cpu_baseline(cfg, budget_s=12.0):
             break
     dt = time.perf_counter() - t0
     return {"value": tokens / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"request 0 of config 2, {tokens} tokens ({tokens // C} epochs of 512): "
+            "sample": f"request 0 of the workload, {tokens} tokens ({tokens // C} epochs of 512): "
                       f"scoring + route + read + route + commit, fp32 scalar C oracle, {dt:.1f} s"}
 
 
@@ -215,8 +247,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, choices=(1, 2, 3), default=2,
+                    help="BASELINE.json configs[config-1]; 2 (the headline) is the default")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--schedule", choices=("serial", "overlap"), default="overlap",
+    ap.add_argument("--schedule", choices=("serial", "overlap"), default="serial",
                     help="serial: every call on one stream; overlap: routes of later epochs on a second stream")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -231,7 +265,7 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
-    cfg = CFG
+    cfg = CONFIGS[args.config]
     pipe = Pipeline(cfg, dev)
     unique = pipe.unique_rows()
     for _ in range(args.warmup):
@@ -308,7 +342,7 @@ def main():
                 "peak": MFMA_BF16_PEAK / 1e12}
         achieved = flops / t_launch / 1e12
         bytes_launch = None
-    traffic = TRAFFIC_PER_LAUNCH.get(dominant)
+    traffic = TRAFFIC_PER_LAUNCH.get(dominant) if args.config == 2 else None
     roof.update({"achieved": round(achieved, 1), "frac": round(achieved / roof["peak"], 4),
                  "traffic": None if traffic is None else int(traffic)})
 
@@ -327,10 +361,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded CPU generator, config-2 protocol)",
-        "config": {"workload": "memory op, BASELINE configs[1]: B=8 T=2048 (4 epochs of 512) H=8 M=65536 "
-                               "dk=128 D=128 k=16 bf16, fused score-route + read + fused score-route + keys + commit",
+        "dtype": "bf16" if cfg["dtype"] == torch.bfloat16 else "f32",
+        "data": "synthetic (seeded CPU generator, BASELINE.json config protocol)",
+        "config": {"workload": f"memory op, BASELINE configs[{args.config - 1}]: B={cfg['B']} T={cfg['T']} "
+                               f"({epochs} epochs of {cfg['C']}) H={cfg['H']} M={cfg['half'] ** 2} dk={cfg['dk']} "
+                               f"D={cfg['D']} k={cfg['k']} {'bf16' if cfg['dtype'] == torch.bfloat16 else 'fp32'}"
+                               f"{' Zipf-skewed' if cfg['skew'] else ''}, fused score-route + read + fused "
+                               "score-route + keys + commit",
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
                    "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
                    "parallelism": "single GPU"},
