@@ -46,10 +46,10 @@ CFG = CONFIGS[2]
 # WRITE x 1.0); source: profiles/glsdm_kernels.config2.hbm-traffic.md.  Re-measured
 # whenever a kernel of the path changes.
 TRAFFIC_PER_LAUNCH = {
-    "score_route": (4972.2 * 1.9998 + 6144.0) * 1024,
-    "read": (67336.2 * 1.9998 + 16384.0) * 1024,
-    "commit": ((10.7 + 2069.7 + 4 * 2525.5 + 138558.9) * 1.9998
-               + (1032.1 + 6301.7 + 4 * 4863.4 + 120899.2)) * 1024,
+    "score_route": (4964.3 * 1.9998 + 6144.0) * 1024,
+    "read": (67334.2 * 1.9998 + 16384.0) * 1024,
+    "commit": ((10.6 + 2069.0 + 3 * 2534.7 + 133287.6) * 1.9998
+               + (776.1 + 4384.0 + 3 * 4933.5 + 120860.8)) * 1024,
 }
 
 
