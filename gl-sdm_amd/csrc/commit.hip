@@ -228,15 +228,68 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
     }
 }
 
+// Where the segment kernel takes each entry's delta row from.
+//
+// StoredDeltas: the materialised deltas [E, D] (fp32 or bf16).
+template <typename TD> struct StoredDeltas {
+    const TD *deltas;
+    int64_t D;
+    struct Entry {
+        const TD *src;
+    };
+    __device__ __forceinline__ Entry entry(int64_t ent) const { return {deltas + ent * D}; }
+    template <int VEC>
+    __device__ __forceinline__ void get(const Entry &e, int v, const float (&)[VEC], float (&x)[VEC]) const
+    {
+        VecLoad<TD, VEC>::load(e.src + (int64_t)v * VEC, x);
+    }
+};
+
+// ProposalTerms: the write-proposal delta of S/runtime/dense.py:11-14,
+//     mass * ((decay - 1) * row + weight * error),
+// evaluated from the row's value before the commit, which is the snapshot row
+// the proposal gathered (S/layers/global_layer.py:44): entry e belongs to
+// proposal row r = e / width, whose error row and decay were computed once,
+// and to mass group r / heads.  Separate fp32 operations in that order.
+struct ProposalTerms {
+    const float *error, *decay, *weights, *mass;
+    int64_t D;
+    uint32_t width, heads;
+    struct Entry {
+        const float *err;
+        float a, w, m;
+    };
+    __device__ __forceinline__ Entry entry(int64_t ent) const
+    {
+#pragma clang fp contract(off)
+        const uint32_t r = (uint32_t)ent / width;
+        return {error + (int64_t)r * D, decay[r] - 1.0f, weights[ent], mass[r / heads]};
+    }
+    template <int VEC>
+    __device__ __forceinline__ void get(const Entry &e, int v, const float (&old)[VEC], float (&x)[VEC]) const
+    {
+#pragma clang fp contract(off)
+        float er[VEC];
+        VecLoad<float, VEC>::load(e.err + (int64_t)v * VEC, er);
+#pragma unroll
+        for (int y = 0; y < VEC; ++y) {
+            const float p = e.a * old[y];
+            const float q = e.w * er[y];
+            const float s = p + q;
+            x[y] = e.m * s;
+        }
+    }
+};
+
 // One wavefront per 64 consecutive sorted positions; lane groups of `lpr` lanes
 // (one bank row each) walk the address runs that start in the wave's window.
-template <typename TB, typename TD, int VEC, int CH>
+template <typename TB, typename SRC, int VEC, int CH>
 __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int64_t rows, int64_t D,
-                                                      const int64_t *__restrict__ keys,
-                                                      const TD *__restrict__ deltas,
+                                                      const int64_t *__restrict__ keys, const SRC src,
                                                       const uint64_t *__restrict__ sorted, int64_t n, int ebits,
                                                       int nv, int lpr, unsigned long long *__restrict__ unique_out)
 {
+#pragma clang fp contract(off)
     __shared__ uint64_t s_w[4][64];
     __shared__ int s_head[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -261,15 +314,15 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
     const int ng = 64 / lpr;
     const int grp = lane / lpr, li = lane % lpr;
     auto word_at = [&](int q) -> uint64_t { return q < 64 ? s_w[wave][q] : sorted[p0 + q]; };
-    auto add_delta = [&](int64_t ent, float (&acc)[CH][VEC]) {
+    auto add_delta = [&](int64_t ent, const float (&old)[CH][VEC], float (&acc)[CH][VEC]) {
         if (ent >= n) return;                           // impossible after a correct sort; never read out of bounds
-        const TD *src = deltas + ent * D;
+        const typename SRC::Entry e = src.entry(ent);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
             if (v < nv) {
                 float x[VEC];
-                VecLoad<TD, VEC>::load(src + (int64_t)v * VEC, x);
+                src.template get<VEC>(e, v, old[c], x);
 #pragma unroll
                 for (int y = 0; y < VEC; ++y) acc[c][y] += x[y];
             }
@@ -289,7 +342,10 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
 #pragma unroll
-            for (int x = 0; x < VEC; ++x) acc[c][x] = 0.0f;     // sums start from +0
+            for (int x = 0; x < VEC; ++x) {
+                acc[c][x] = 0.0f;                               // sums start from +0
+                old[c][x] = 0.0f;
+            }
             if (v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
         }
         // arrival order is key order unless a later entry has a smaller key
@@ -307,7 +363,7 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
             }
         }
         if (in_order) {
-            for (int q = 0; q < len; ++q) add_delta((int64_t)(word_at(h + q) & emask), acc);
+            for (int q = 0; q < len; ++q) add_delta((int64_t)(word_at(h + q) & emask), old, acc);
         } else {
             // exact (key, entry) order by repeated selection of the next smallest pair
             int64_t last_k = INT64_MIN, last_e = -1;
@@ -321,7 +377,7 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
                     const bool before = k < best_k || (k == best_k && e < best_e);
                     if (after && before) { best_k = k; best_e = e; }
                 }
-                add_delta(best_e, acc);
+                add_delta(best_e, old, acc);
                 last_k = best_k;
                 last_e = best_e;
             }
@@ -338,41 +394,45 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
     }
 }
 
-template <typename TB, typename TD, int VEC>
-static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t *keys,
-                             const void *deltas, const uint64_t *sorted, int64_t n, int ebits,
-                             const RowPlan &p, int64_t *unique_out, hipStream_t st)
+template <typename TB, int VEC, typename SRC>
+static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
+                             const uint64_t *sorted, int64_t n, int ebits, const RowPlan &p,
+                             int64_t *unique_out, hipStream_t st)
 {
     const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
     TB *bk = static_cast<TB *>(bank);
-    const TD *dl = static_cast<const TD *>(deltas);
     auto *u = reinterpret_cast<unsigned long long *>(unique_out);
+#define GLSDM_SEG_LAUNCH(C)                                                                                    \
+    hipLaunchKernelGGL((segment_kernel<TB, SRC, VEC, C>), grid, block, 0, st, bk, rows, D, keys, src, sorted, n, \
+                       ebits, p.nv, p.lpr, u)
     switch (p.ch) {
-    case 1: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 1>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
-    case 2: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 2>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
+    case 1: GLSDM_SEG_LAUNCH(1); break;
+    case 2: GLSDM_SEG_LAUNCH(2); break;
     case 3:
-    case 4: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 4>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
-    default: hipLaunchKernelGGL((segment_kernel<TB, TD, VEC, 8>), grid, block, 0, st, bk, rows, D, keys, dl, sorted, n, ebits, p.nv, p.lpr, u); break;
+    case 4: GLSDM_SEG_LAUNCH(4); break;
+    default: GLSDM_SEG_LAUNCH(8); break;
     }
+#undef GLSDM_SEG_LAUNCH
     return check_launch("segment_kernel");
 }
 
-template <typename TB, typename TD>
-static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys,
-                            const void *deltas, const uint64_t *sorted, int64_t n, int ebits,
+// One vector width for bank and delta rows: the wider element type's 16-byte
+// vector when D and the row pointers allow it, else scalar accesses.
+template <typename TB, typename TD, typename SRC>
+static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
+                            const void *delta_rows, const uint64_t *sorted, int64_t n, int ebits,
                             int64_t *unique_out, hipStream_t st)
 {
-    // One vector width for both operands: the wider type's 16-byte vector.
     constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
-    const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(deltas)) & 15) == 0;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(delta_rows)) & 15) == 0;
     if (D % VEC == 0 && aligned) {
         RowPlan p{VEC, (int)(D / VEC), 0, 0};
         p.lpr = pow2_ceil(p.nv) < 64 ? pow2_ceil(p.nv) : 64;
         p.ch = (int)ceil_div(p.nv, p.lpr);
-        return launch_segment_ch<TB, TD, VEC>(bank, rows, D, keys, deltas, sorted, n, ebits, p, unique_out, st);
+        return launch_segment_ch<TB, VEC>(bank, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
     }
     RowPlan p{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
-    return launch_segment_ch<TB, TD, 1>(bank, rows, D, keys, deltas, sorted, n, ebits, p, unique_out, st);
+    return launch_segment_ch<TB, 1>(bank, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
 }
 
 }  // namespace glsdm
@@ -398,27 +458,31 @@ extern "C" int glsdm_commit_workspace_bytes(int64_t entries, int64_t rows, size_
     return GLSDM_OK;
 }
 
-extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
-                            const int64_t *addresses, const void *deltas, int32_t delta_dtype,
-                            const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
-                            int64_t *unique_out, void *stream)
+// Shape checks shared by both commit entry points; entries > 0.
+static int check_commit(const char *what, int64_t rows, int64_t D, int64_t entries)
 {
-    if (rows < 1 || D < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit: bad shape rows=%lld D=%lld entries=%lld", (long long)rows, (long long)D, (long long)entries);
-    if (!dtype_ok(bank_dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "commit: bad dtype");
-    if (entries == 0) return GLSDM_OK;
-    if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "commit: more than 2^30 entries");
-    if (!bank || !addresses || !deltas) return fail(GLSDM_ERR_ARG, "commit: null pointer");
-    if (D > 512 && D % 8 != 0) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld not a multiple of 8 above 512", (long long)D);
-    if (D > 64 * 8 * 4) return fail(GLSDM_ERR_UNSUPPORTED, "commit: D=%lld above 2048", (long long)D);
+    if (entries > MAX_ENTRIES) return fail(GLSDM_ERR_UNSUPPORTED, "%s: more than 2^30 entries", what);
+    if (D > 512 && D % 8 != 0)
+        return fail(GLSDM_ERR_UNSUPPORTED, "%s: D=%lld not a multiple of 8 above 512", what, (long long)D);
+    if (D > 64 * 8 * 4) return fail(GLSDM_ERR_UNSUPPORTED, "%s: D=%lld above 2048", what, (long long)D);
+    if (address_bits(rows) + entry_bits(entries) > 64)
+        return fail(GLSDM_ERR_UNSUPPORTED, "%s: address bits %d + entry bits %d exceed 64", what,
+                    address_bits(rows), entry_bits(entries));
+    return GLSDM_OK;
+}
+
+// Steps 1-3 of the pipeline: the packed (address, entry) words sorted by
+// address, in *sorted (one of the two workspace word buffers).
+static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
+                       size_t workspace_bytes, const char *what, const uint64_t **sorted, int *ebits_out,
+                       hipStream_t st)
+{
     const int ebits = entry_bits(entries), abits = address_bits(rows);
-    if (abits + ebits > 64)
-        return fail(GLSDM_ERR_UNSUPPORTED, "commit: address bits %d + entry bits %d exceed 64", abits, ebits);
     const int passes = pass_count(abits);
     CommitWorkspace ws = plan_workspace(workspace, entries, passes);
     if (!workspace || workspace_bytes < ws.bytes)
-        return fail(GLSDM_ERR_WORKSPACE, "commit: workspace of %zu bytes needed, %zu given", ws.bytes, workspace_bytes);
-    const hipStream_t st = as_stream(stream);
-
+        return fail(GLSDM_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, ws.bytes,
+                    workspace_bytes);
     const unsigned prep_blocks = (unsigned)std::max<int64_t>(
         std::min<int64_t>(ceil_div((int64_t)ws.status_words, 256), 4096), (MAX_PASSES * RADIX) / 256);
     hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
@@ -437,12 +501,72 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
         if ((rc = check_launch("onesweep_kernel"))) return rc;
         uint64_t *t = src; src = dst; dst = t;
     }
+    *sorted = src;
+    *ebits_out = ebits;
+    return GLSDM_OK;
+}
 
+template <typename TB, typename TD>
+static int segment_stored(void *bank, int64_t rows, int64_t D, const int64_t *keys, const void *deltas,
+                          const uint64_t *sorted, int64_t n, int ebits, int64_t *unique_out, hipStream_t st)
+{
+    const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};
+    return launch_segment_t<TB, TD>(bank, rows, D, keys, src, deltas, sorted, n, ebits, unique_out, st);
+}
+
+extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                            const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                            const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
+                            int64_t *unique_out, void *stream)
+{
+    if (rows < 1 || D < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit: bad shape rows=%lld D=%lld entries=%lld", (long long)rows, (long long)D, (long long)entries);
+    if (!dtype_ok(bank_dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "commit: bad dtype");
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("commit", rows, D, entries);
+    if (rc) return rc;
+    if (!bank || !addresses || !deltas) return fail(GLSDM_ERR_ARG, "commit: null pointer");
+    const hipStream_t st = as_stream(stream);
+    const uint64_t *sorted = nullptr;
+    int ebits = 0;
+    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit", &sorted, &ebits, st)))
+        return rc;
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
-        return launch_segment_t<float, float>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
+        return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
-        return launch_segment_t<float, bf16_t>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
+        return segment_stored<float, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
     if (bank_dtype == GLSDM_BF16 && delta_dtype == GLSDM_F32)
-        return launch_segment_t<bf16_t, float>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
-    return launch_segment_t<bf16_t, bf16_t>(bank, rows, D, keys, deltas, src, entries, ebits, unique_out, st);
+        return segment_stored<bf16_t, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
+    return segment_stored<bf16_t, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
+}
+
+extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                                      const int64_t *addresses, const int64_t *keys, int64_t entries, int32_t width,
+                                      const float *weights, const float *error, const float *decay,
+                                      const float *mass, int64_t heads, void *workspace, size_t workspace_bytes,
+                                      int64_t *unique_out, void *stream)
+{
+    if (rows < 1 || D < 1 || entries < 0 || width < 1 || heads < 1)
+        return fail(GLSDM_ERR_ARG, "commit_proposals: bad shape rows=%lld D=%lld entries=%lld width=%d heads=%lld",
+                    (long long)rows, (long long)D, (long long)entries, (int)width, (long long)heads);
+    if (!dtype_ok(bank_dtype)) return fail(GLSDM_ERR_ARG, "commit_proposals: bad dtype");
+    if (entries % width != 0 || (entries / width) % heads != 0)
+        return fail(GLSDM_ERR_ARG, "commit_proposals: %lld entries are not whole rows of width %d and %lld heads",
+                    (long long)entries, (int)width, (long long)heads);
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("commit_proposals", rows, D, entries);
+    if (rc) return rc;
+    if (!bank || !addresses || !weights || !error || !decay || !mass)
+        return fail(GLSDM_ERR_ARG, "commit_proposals: null pointer");
+    const hipStream_t st = as_stream(stream);
+    const uint64_t *sorted = nullptr;
+    int ebits = 0;
+    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit_proposals", &sorted,
+                          &ebits, st)))
+        return rc;
+    const ProposalTerms src{error, decay, weights, mass, D, (uint32_t)width, (uint32_t)heads};
+    if (bank_dtype == GLSDM_F32)
+        return launch_segment_t<float, float>(bank, rows, D, keys, src, error, sorted, entries, ebits,
+                                              unique_out, st);
+    return launch_segment_t<bf16_t, float>(bank, rows, D, keys, src, error, sorted, entries, ebits, unique_out,
+                                           st);
 }

@@ -4,7 +4,9 @@ Mirrors S/memory/__init__.py (S/ = projects/gl-sdm/src/gl_sdm/).  The
 token-clock ``read``/``propose_write`` of the reference are not on the stack's
 path and are not provided.
 """
-from .state import MemoryView, WriteProposal, WriteBuffer, MemoryCache, MemoryBank
+from .state import MemoryView, WriteProposal, DeferredProposal, WriteBuffer, MemoryCache, MemoryBank
 from .transactions import merge, commit
+from .proposals import layer_proposal
 
-__all__ = ["MemoryView", "WriteProposal", "WriteBuffer", "MemoryCache", "MemoryBank", "merge", "commit"]
+__all__ = ["MemoryView", "WriteProposal", "DeferredProposal", "WriteBuffer", "MemoryCache", "MemoryBank",
+           "merge", "commit", "layer_proposal"]

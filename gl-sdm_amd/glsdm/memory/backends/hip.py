@@ -12,6 +12,9 @@ this module                reference entry point it stands in for
 ``gather_rows``            ``S/memory/routing.py:37-42``, ``primitives.py:15-20``
 ``proposal_keys``          ``S/layers/global_layer.py:45,52-53``
 ``score``                  ``S/layers/global_layer.py:26,42`` (per-head form)
+``proposal_delta``         ``S/runtime/dense.py:11-14``
+``proposal_error``         ``S/runtime/dense.py:12-13`` (decay and error terms)
+``commit_proposals``       ``dense.py:11-14`` + ``global_layer.py:44`` + ``commit``
 ``require_cuda``           ``S/memory/backends/primitives.py:7-12``
 =========================  ===================================================
 
@@ -178,6 +181,18 @@ def gather_rows(values, index):
     return out
 
 
+def gather_flat(values, addresses):
+    """Rows ``[*addresses.shape, D]`` of ``values`` viewed as ``[rows, D]`` at absolute ``addresses``."""
+    device = require_cuda(values, addresses)
+    if addresses.dtype != torch.int64:
+        raise ValueError("gather_flat needs int64 addresses")
+    D = values.shape[-1]
+    out = torch.empty((*addresses.shape, D), dtype=values.dtype, device=device)
+    N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), values.numel() // D, D, N.ptr(addresses),
+           addresses.numel(), N.ptr(out), N.stream(device))
+    return out
+
+
 def commit_workspace_bytes(entries, rows):
     size = N.ctypes.c_size_t(0)
     N.call("glsdm_commit_workspace_bytes", entries, rows, N.ctypes.byref(size))
@@ -216,4 +231,94 @@ def commit(memory, indices, deltas, keys=None, donate=False, workspace=None, uni
     N.call("glsdm_commit", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(deltas),
            N.dtype_code(deltas), N.ptr(keys), E, N.ptr(workspace), workspace.numel(), N.ptr(unique),
            N.stream(device))
+    return out
+
+
+def _proposal_rows(prediction, target, beta, log_decay):
+    """Shapes of the per-row proposal operands: prediction/target ``[..., H, D]``,
+    beta/log_decay ``[..., H, 1]`` -> (R, H, D)."""
+    if prediction.ndim < 2 or target.shape != prediction.shape:
+        raise ValueError("proposal needs prediction and target of one shape [..., H, D]")
+    if prediction.dtype != torch.float32 or target.dtype not in N.DTYPES:
+        raise ValueError("proposal needs fp32 prediction and fp32 or bf16 target")
+    lead = prediction.shape[:-1]
+    for t in (beta, log_decay):
+        if t.dtype != torch.float32 or t.shape not in ((*lead, 1), lead):
+            raise ValueError("proposal needs fp32 beta and log_decay of shape [..., H, 1]")
+    D = prediction.shape[-1]
+    return prediction.numel() // D, prediction.shape[-2], D
+
+
+def proposal_error(prediction, target, beta, log_decay):
+    """``(error [..., H, D] fp32, decay [..., H] fp32)``: decay = exp(log_decay),
+    error = beta * (target - decay * prediction), the per-row terms of dense.py:12-13."""
+    _no_grad(prediction, target, beta, log_decay)
+    device = require_cuda(prediction, target, beta, log_decay)
+    R, _, D = _proposal_rows(prediction, target, beta, log_decay)
+    error = torch.empty(prediction.shape, dtype=torch.float32, device=device)
+    decay = torch.empty(prediction.shape[:-1], dtype=torch.float32, device=device)
+    N.call("glsdm_proposal_error", R, D, N.ptr(prediction), N.ptr(target), N.dtype_code(target), N.ptr(beta),
+           N.ptr(log_decay), N.ptr(error), N.ptr(decay), N.stream(device))
+    return error, decay
+
+
+def proposal_delta(rows, weights, prediction, target, beta, log_decay, mass):
+    """Write deltas ``[..., H, k, D]`` fp32 of dense.py:11-14:
+    ``mass * ((exp(log_decay) - 1) * rows + weights * beta * (target - exp(log_decay) * prediction))``."""
+    _no_grad(rows, weights, prediction, target, beta, log_decay, mass)
+    device = require_cuda(rows, weights, prediction, target, beta, log_decay, mass)
+    R, H, D = _proposal_rows(prediction, target, beta, log_decay)
+    lead = prediction.shape[:-2]
+    if rows.ndim != prediction.ndim + 1 or rows.shape[:-2] != prediction.shape[:-1] or rows.shape[-1] != D:
+        raise ValueError("proposal_delta needs rows [..., H, k, D] matching the prediction")
+    k = rows.shape[-2]
+    if weights.shape != rows.shape[:-1] or weights.dtype != torch.float32 or rows.dtype not in N.DTYPES:
+        raise ValueError("proposal_delta needs fp32 weights [..., H, k] and fp32 or bf16 rows")
+    if mass.shape != lead or mass.dtype != torch.float32:
+        raise ValueError("proposal_delta needs fp32 mass of the leading shape [...]")
+    out = torch.empty(rows.shape, dtype=torch.float32, device=device)
+    N.call("glsdm_proposal_delta", N.ptr(rows), N.dtype_code(rows), R, k, D, N.ptr(weights), N.ptr(prediction),
+           N.ptr(target), N.dtype_code(target), N.ptr(beta), N.ptr(log_decay), N.ptr(mass), H, N.ptr(out),
+           N.stream(device))
+    return out
+
+
+def commit_proposals(memory, indices, keys, weights, error, decay, mass, donate=False, workspace=None,
+                     unique=None):
+    """Fused proposal -> commit: commits the deltas
+    ``mass[r // H] * ((decay[r] - 1) * memory[indices[e]] + weights[e] * error[r])``, ``r = e // k``,
+    evaluated in the commit from each touched row (never stored).
+
+    ``indices``/``keys``/``weights`` ``[..., H, k]`` (absolute rows, collision
+    keys or None, route weights), ``error [..., H, D]`` and ``decay [..., H]``
+    from :func:`proposal_error`, ``mass`` of the leading shape ``[...]``.  The
+    rows must be those the proposal was made against (``memory`` is its
+    snapshot).  Bitwise equal to ``commit(memory, indices, proposal_delta(...), keys)``.
+    """
+    _no_grad(memory, weights, error, decay, mass)
+    device = require_cuda(memory, indices, keys, weights, error, decay, mass)
+    D = memory.shape[-1]
+    if indices.dtype != torch.int64 or (keys is not None and (keys.dtype != torch.int64
+                                                               or keys.shape != indices.shape)):
+        raise ValueError("commit_proposals needs int64 addresses and keys of one shape")
+    if indices.ndim < 2 or weights.shape != indices.shape or weights.dtype != torch.float32:
+        raise ValueError("commit_proposals needs fp32 weights [..., H, k] matching the addresses")
+    H, k = indices.shape[-2], indices.shape[-1]
+    if (error.shape != (*indices.shape[:-1], D) or decay.shape != indices.shape[:-1]
+            or mass.shape != indices.shape[:-2]):
+        raise ValueError("commit_proposals needs error [..., H, D], decay [..., H] and mass [...] "
+                         "matching the addresses [..., H, k]")
+    if error.dtype != torch.float32 or decay.dtype != torch.float32 or mass.dtype != torch.float32:
+        raise ValueError("commit_proposals needs fp32 error, decay and mass")
+    out = memory if donate else memory.clone()
+    E = indices.numel()
+    if E == 0:
+        return out
+    rows = memory.numel() // D
+    need = commit_workspace_bytes(E, rows)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    N.call("glsdm_commit_proposals", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(keys), E, k,
+           N.ptr(weights), N.ptr(error), N.ptr(decay), N.ptr(mass), H, N.ptr(workspace), workspace.numel(),
+           N.ptr(unique), N.stream(device))
     return out

@@ -1,0 +1,34 @@
+"""Write proposals of one global layer on the HIP path.
+
+Mirrors the proposal construction of ``GlobalLayer.propose``
+(S/layers/global_layer.py:33-54, S/ = projects/gl-sdm/src/gl_sdm/) after its
+write route: addresses and collision keys ``addr*(C*L) + position*L + layer``
+(:45,52-53), ``mass = 1`` per token (:50), and the deltas of
+S/runtime/dense.py:11-14 against the snapshot rows the route selected (:44).
+
+``deferred=True`` (default) returns a :class:`DeferredProposal`, whose deltas
+are evaluated inside the commit from the rows it touches (the ``[E, D]``
+deltas and the row re-gather are never materialised); ``deferred=False``
+returns the reference's :class:`WriteProposal` with fp32 deltas.
+"""
+import torch
+
+from .state import DeferredProposal, WriteProposal
+from .backends import hip
+
+
+def layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
+                   chunk_size, num_layers, mass=None, deferred=True):
+    """Proposal of the write route ``index``/``weights [B, T, H, k]`` with its routed
+    read ``prediction [B, T, H, D]``, value ``target [B, T, H, D]`` and gates
+    ``beta``/``log_decay [B, T, H, 1]`` (``mass [B, T]``, default ones)."""
+    addresses, keys = hip.proposal_keys(snapshot.values, index, offset, chunk_size, num_layers, layer_idx)
+    if mass is None:
+        mass = torch.ones(index.shape[:2], dtype=torch.float32, device=index.device)
+    if deferred:
+        return DeferredProposal(snapshot.version, addresses, weights, prediction, target, beta, log_decay, mass,
+                                snapshot.lineage, keys)
+    rows = hip.gather_rows(snapshot.values, index)
+    delta = hip.proposal_delta(rows, weights, prediction, target, beta, log_decay, mass)
+    return WriteProposal(snapshot.version, addresses.flatten(), delta.flatten(0, 3), snapshot.lineage,
+                         keys.flatten())

@@ -35,6 +35,39 @@ class WriteProposal:
 
 
 @dataclass(frozen=True)
+class DeferredProposal:
+    """A write proposal whose deltas are evaluated inside the commit.
+
+    Holds the operands of S/runtime/dense.py:11-14 except the gathered rows:
+    the commit reads each touched row once anyway, and that row (before the
+    commit) is the snapshot row the reference gathers at
+    S/layers/global_layer.py:44, so ``mass * ((exp(log_decay) - 1) * row +
+    weights * beta * (target - exp(log_decay) * prediction))`` is formed there
+    and the ``[E, D]`` deltas are never stored.  Shapes: addresses, weights and
+    sort_keys ``[..., H, k]``; prediction/target ``[..., H, D]``;
+    beta/log_decay ``[..., H, 1]``; mass ``[...]``.
+    """
+    base_version: int
+    addresses: torch.Tensor   # absolute rows, int64
+    weights: torch.Tensor     # route weights, fp32
+    prediction: torch.Tensor  # routed read of the write route, fp32
+    target: torch.Tensor      # fp32 or bf16
+    beta: torch.Tensor        # fp32
+    log_decay: torch.Tensor   # fp32
+    mass: torch.Tensor        # fp32
+    lineage: object
+    sort_keys: torch.Tensor | None = None
+
+    @property
+    def heads(self):
+        return self.addresses.shape[-2]
+
+    @property
+    def width(self):
+        return self.addresses.shape[-1]
+
+
+@dataclass(frozen=True)
 class WriteBuffer:
     base_version: int
     proposals: tuple

@@ -8,7 +8,7 @@ place instead of returning a new bank (the old view must not be used again).
 """
 import torch
 
-from .state import MemoryView, WriteBuffer
+from .state import DeferredProposal, MemoryView, WriteBuffer
 from .backends import hip
 
 BACKENDS = ("hip",)
@@ -32,6 +32,33 @@ def _cat(tensors):
     return tensors[0] if len(tensors) == 1 else torch.cat(tensors)
 
 
+def _materialise(values, p):
+    """Deltas [E, D] of a deferred proposal against the snapshot ``values``."""
+    D = values.shape[-1]
+    rows = hip.gather_flat(values, p.addresses)
+    return hip.proposal_delta(rows, p.weights, p.prediction, p.target, p.beta, p.log_decay,
+                              p.mass).reshape(-1, D)
+
+
+def _commit_deferred(view, props, keys, donate):
+    """All proposals deferred with one (heads, width): one fused commit."""
+    H, k = props[0].heads, props[0].width
+    lead = lambda t, tail: t.reshape(-1, *tail)
+    idx = _cat([lead(p.addresses, (H, k)) for p in props])
+    weights = _cat([lead(p.weights, (H, k)) for p in props])
+    pred = _cat([lead(p.prediction, (H, p.prediction.shape[-1])) for p in props])
+    targets = [lead(p.target, (H, p.target.shape[-1])) for p in props]
+    if len({t.dtype for t in targets}) > 1:
+        targets = [t.float() for t in targets]
+    beta = _cat([lead(p.beta, (H, 1)) for p in props])
+    log_decay = _cat([lead(p.log_decay, (H, 1)) for p in props])
+    mass = _cat([p.mass.reshape(-1) for p in props])
+    error, decay = hip.proposal_error(pred.contiguous(), _cat(targets).contiguous(), beta.contiguous(),
+                                      log_decay.contiguous())
+    return hip.commit_proposals(view.values, idx.contiguous(), None if keys is None else keys.reshape(idx.shape),
+                                weights.contiguous(), error, decay, mass.contiguous(), donate=donate)
+
+
 def commit(view, buffer, reference=False, backend="hip", donate=False):
     _check_backend(backend, reference)
     if buffer.base_version != view.version or buffer.lineage is not view.lineage:
@@ -40,15 +67,18 @@ def commit(view, buffer, reference=False, backend="hip", donate=False):
     keyed = [p.sort_keys is not None for p in props]
     if any(keyed) and not all(keyed):
         raise ValueError("cannot mix keyed and unkeyed proposals")
+    # unkeyed proposals collide in arrival order: the reference sorts them by address
+    # with a stable sort, which keeps arrival order within an address
+    keys = _cat([p.sort_keys.reshape(-1) for p in props]).contiguous() if all(keyed) else None
+    deferred = [isinstance(p, DeferredProposal) for p in props]
+    if all(deferred) and len({(p.heads, p.width) for p in props}) == 1:
+        updated = _commit_deferred(view, props, keys, donate)
+        return MemoryView(updated, view.version + 1, view.lineage)
     idx = _cat([p.addresses.reshape(-1) for p in props])
     D = view.values.shape[-1]
-    deltas = [p.deltas.reshape(-1, D) for p in props]
+    deltas = [_materialise(view.values, p) if d else p.deltas.reshape(-1, D) for p, d in zip(props, deferred)]
     if len({d.dtype for d in deltas}) > 1:
         deltas = [d.float() for d in deltas]
     delta = _cat(deltas)
-    # unkeyed proposals collide in arrival order: the reference sorts them by address
-    # with a stable sort, which keeps arrival order within an address
-    keys = _cat([p.sort_keys.reshape(-1) for p in props]) if all(keyed) else None
-    updated = hip.commit(view.values, idx.contiguous(), delta.contiguous(),
-                         None if keys is None else keys.contiguous(), donate=donate)
+    updated = hip.commit(view.values, idx.contiguous(), delta.contiguous(), keys, donate=donate)
     return MemoryView(updated, view.version + 1, view.lineage)

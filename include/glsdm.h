@@ -175,6 +175,60 @@ int glsdm_proposal_keys(const int64_t *index, int64_t B, int64_t T, int64_t H, i
 int glsdm_gather_rows(const void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
                       const int64_t *addresses, int64_t n, void *out, void *stream);
 
+/*
+ * Per-row terms of a write proposal, for R proposal rows (r = token*H + h):
+ *   decay[r]    = exp(log_decay[r])
+ *   error[r, :] = beta[r] * (target[r, :] - decay[r] * prediction[r, :])
+ * prediction [R, D] fp32 (the routed read of the write route), target [R, D]
+ * of target_dtype, beta/log_decay [R] fp32; outputs error [R, D] fp32 and
+ * decay [R] fp32.  Separate fp32 operations in the reference's order.
+ * Replaces: the decay and error lines of S/runtime/dense.py:12-13
+ * (proposal_delta), whose operands S/layers/global_layer.py:42-50 builds.
+ */
+int glsdm_proposal_error(int64_t R, int64_t D, const float *prediction, const void *target,
+                         int32_t target_dtype, const float *beta, const float *log_decay,
+                         float *error, float *decay, void *stream);
+
+/*
+ * Materialised write-proposal deltas, for R proposal rows of `width` entries:
+ *   deltas[r, j, :] = mass[r / heads] * ((decay[r] - 1) * rows[r, j, :]
+ *                                        + weights[r, j] * error[r, :])
+ * with decay and error as in glsdm_proposal_error.  rows [R, width, D] of
+ * rows_dtype (the gathered snapshot rows), weights [R, width] fp32, mass
+ * [R / heads] fp32 (one value per token), deltas [R, width, D] fp32.
+ * Replaces: S/runtime/dense.py:11-14 (proposal_delta), with rows, weights,
+ * prediction, target, beta, log_decay and mass of shapes [..., H, k, D],
+ * [..., H, k], [..., H, D], [..., H, D], [..., H, 1], [..., H, 1], [...].
+ */
+int glsdm_proposal_delta(const void *rows, int32_t rows_dtype, int64_t R, int32_t width, int64_t D,
+                         const float *weights, const float *prediction, const void *target,
+                         int32_t target_dtype, const float *beta, const float *log_decay,
+                         const float *mass, int64_t heads, float *deltas, void *stream);
+
+/*
+ * Fused proposal -> commit, in place on `bank`: glsdm_commit of the deltas
+ *   delta[e, :] = mass[r / heads] * ((decay[r] - 1) * bank[addresses[e], :]
+ *                                    + weights[e] * error[r, :]),  r = e / width,
+ * evaluated inside the commit from each touched row's value before the
+ * commit, so the deltas [entries, D] are never stored.  error/decay come from
+ * glsdm_proposal_error; weights [entries] fp32, mass [entries / width / heads].
+ * entries must be a multiple of width * heads.  The result is bitwise that of
+ * glsdm_proposal_delta on the gathered rows followed by glsdm_commit, when the
+ * bank is the snapshot the proposal gathered its rows from (the reference
+ * commits only against that version: S/memory/transactions.py:72-73).
+ * Several proposals (layers) of equal width and heads are committed together
+ * by concatenating their entries, rows of error/decay, and mass.
+ * Workspace: glsdm_commit_workspace_bytes(entries, rows).
+ * Replaces: S/runtime/dense.py:11-14 (proposal_delta) with
+ * S/layers/global_layer.py:44 (gather_rows) feeding
+ * S/memory/transactions.py:69-97 (commit) through S/layers/stack.py:65.
+ */
+int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                           const int64_t *addresses, const int64_t *keys, int64_t entries, int32_t width,
+                           const float *weights, const float *error, const float *decay,
+                           const float *mass, int64_t heads, void *workspace, size_t workspace_bytes,
+                           int64_t *unique_out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@ function               reference (``S/`` = ``projects/gl-sdm/src/gl_sdm/``)
 ``commit``             ``S/memory/transactions.py:69-97`` (torch branch)
 ``commit_dense``       ``S/memory/transactions.py:85-88`` (reference=True branch)
 ``proposal_delta``     ``S/runtime/dense.py:11-14``
+``proposal_error``     ``S/runtime/dense.py:13`` (the error row alone)
 =====================  ==========================================================
 
 Pinning (see ``tests/test_oracle.py``): known answers copied as data from the
@@ -132,8 +133,17 @@ def commit_bf16(flat_bf16, addresses, deltas, keys=None):
     return commit(flat_bf16.float(), addresses, deltas, keys).to(torch.bfloat16)
 
 
-def proposal_delta(rows, weights, prediction, target, beta, log_decay, mass):
-    """Write delta of one proposal, same operation order as dense.py:11-14."""
-    g = log_decay.exp()
-    err = beta * (target.float() - g * prediction)
+def proposal_error(prediction, target, beta, decay):
+    """Error row ``beta * (target - decay * prediction)`` of dense.py:13."""
+    return beta * (target.float() - decay * prediction)
+
+
+def proposal_delta(rows, weights, prediction, target, beta, log_decay, mass, decay=None):
+    """Write delta of one proposal, same operation order as dense.py:11-14.
+
+    ``decay`` (``[..., H, 1]``) replaces ``log_decay.exp()`` when given, so a
+    test can hold the exponential fixed and compare the rest bitwise.
+    """
+    g = log_decay.exp() if decay is None else decay
+    err = proposal_error(prediction, target, beta, g)
     return mass[..., None, None, None] * ((g[..., None] - 1) * rows + weights[..., None] * err[..., None, :])

@@ -12,7 +12,8 @@ def test_header_declares_the_expected_surface():
     names = header_functions()
     for required in ("glsdm_route", "glsdm_read", "glsdm_route_read", "glsdm_score", "glsdm_commit",
                      "glsdm_commit_workspace_bytes", "glsdm_absolute_addresses", "glsdm_proposal_keys",
-                     "glsdm_gather_rows", "glsdm_version", "glsdm_last_error"):
+                     "glsdm_gather_rows", "glsdm_version", "glsdm_last_error", "glsdm_proposal_error",
+                     "glsdm_proposal_delta", "glsdm_commit_proposals"):
         assert required in names
 
 
@@ -50,6 +51,30 @@ def test_commit_workspace_contract():
     assert _rc("glsdm_commit", ctypes.c_void_p(1), 0, 16, 4, ctypes.c_void_p(1), ctypes.c_void_p(1), 0,
                None, 8, None, 0, None, None) == N.ERR_WORKSPACE
     assert _rc("glsdm_commit", None, 0, 16, 4, None, None, 0, None, 0, None, 0, None, None) == N.OK
+
+
+def test_proposal_envelopes():
+    one = ctypes.c_void_p(16)
+    # D above the supported row width, D not a multiple of 4 above 512
+    assert _rc("glsdm_proposal_error", 4, 4096, one, one, 0, one, one, one, one, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_proposal_error", 4, 514, one, one, 0, one, one, one, one, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_proposal_error", 4, 64, one, one, 3, one, one, one, one, None) == N.ERR_ARG   # dtype
+    assert _rc("glsdm_proposal_error", 4, 64, None, one, 0, one, one, one, one, None) == N.ERR_ARG  # null
+    assert _rc("glsdm_proposal_error", 0, 64, None, None, 0, None, None, None, None, None) == N.OK
+    # R must be whole groups of heads (mass has one value per token)
+    assert _rc("glsdm_proposal_delta", one, 0, 6, 2, 64, one, one, one, 0, one, one, one, 4, one,
+               None) == N.ERR_ARG
+    assert _rc("glsdm_proposal_delta", one, 0, 8, 0, 64, one, one, one, 0, one, one, one, 4, one,
+               None) == N.ERR_ARG
+    # fused commit: entries must be whole proposal rows, workspace checked before launch
+    assert _rc("glsdm_commit_proposals", one, 0, 16, 4, one, None, 10, 4, one, one, one, one, 1, None, 0,
+               None, None) == N.ERR_ARG
+    assert _rc("glsdm_commit_proposals", one, 0, 16, 4, one, None, 8, 4, one, one, one, one, 1, None, 0,
+               None, None) == N.ERR_WORKSPACE
+    assert _rc("glsdm_commit_proposals", one, 0, 16, 4, one, None, 8, 4, None, one, one, one, 1, None, 0,
+               None, None) == N.ERR_ARG
+    assert _rc("glsdm_commit_proposals", None, 0, 16, 4, None, None, 0, 4, None, None, None, None, 1, None, 0,
+               None, None) == N.OK
 
 
 def test_read_and_score_envelopes():

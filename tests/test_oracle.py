@@ -183,17 +183,55 @@ def test_planted_mistakes_are_caught():
     assert pairwise != c["expect"][0]
 
 
+def _proposal_operands(seed, lead=(2, 3), H=2, k=4, D=5):
+    g = gen(seed)
+    rows = torch.randn(*lead, H, k, D, generator=g)
+    w = torch.randn(*lead, H, k, generator=g).softmax(-1)
+    pred = torch.randn(*lead, H, D, generator=g)
+    tgt = torch.randn(*lead, H, D, generator=g)
+    beta = torch.rand(*lead, H, 1, generator=g)
+    ld = -torch.rand(*lead, H, 1, generator=g)
+    mass = torch.rand(*lead, generator=g)
+    return rows, w, pred, tgt, beta, ld, mass
+
+
 def test_proposal_delta_closed_form():
-    g = gen(4)
-    rows = torch.randn(2, 3, 2, 4, 5, generator=g)
-    w = torch.randn(2, 3, 2, 4, generator=g).softmax(-1)
-    pred = torch.randn(2, 3, 2, 5, generator=g)
-    tgt = torch.randn(2, 3, 2, 5, generator=g)
-    beta = torch.rand(2, 3, 2, 1, generator=g)
-    ld = -torch.rand(2, 3, 2, 1, generator=g)
-    mass = torch.rand(2, 3, generator=g)
+    rows, w, pred, tgt, beta, ld, mass = _proposal_operands(4)
     out = torch_oracle.proposal_delta(rows, w, pred, tgt, beta, ld, mass)
     gd = ld.double().exp()
     ref = mass.double()[..., None, None, None] * ((gd[..., None] - 1) * rows.double()
           + w.double()[..., None] * (beta.double() * (tgt.double() - gd * pred.double()))[..., None, :])
     torch.testing.assert_close(out.double(), ref, atol=1e-6, rtol=1e-5)
+
+
+def test_proposal_delta_elementwise_rounding():
+    """Each element is the fp32 result of the reference's five roundings in order
+    (scalar numpy float32 arithmetic, one rounding per operation, no FMA)."""
+    np = pytest.importorskip("numpy")
+    rows, w, pred, tgt, beta, ld, mass = _proposal_operands(5, lead=(3,), H=2, k=3, D=4)
+    g = ld.exp()
+    out = torch_oracle.proposal_delta(rows, w, pred, tgt, beta, ld, mass, decay=g)
+    f = np.float32
+    for b in range(3):
+        for h in range(2):
+            gg = f(g[b, h, 0].item())
+            for j in range(3):
+                for d in range(4):
+                    err = f(beta[b, h, 0].item()) * (f(tgt[b, h, d].item()) - gg * f(pred[b, h, d].item()))
+                    x = f(mass[b].item()) * ((gg - f(1)) * f(rows[b, h, j, d].item()) + f(w[b, h, j].item()) * err)
+                    assert np.float32(out[b, h, j, d].item()) == x
+
+
+def test_proposal_delta_rule_invariants():
+    """The delta rule's fixed points: a single full-weight write with beta = 1
+    whose prediction is the written row moves the row to the target; beta = 0
+    only decays it (row + delta = decay * row); mass 0 writes nothing."""
+    rows, w, pred, tgt, beta, ld, mass = _proposal_operands(6, k=1)
+    w = torch.ones_like(w)
+    one = torch.ones_like(beta)
+    new = rows + torch_oracle.proposal_delta(rows, w, rows[..., 0, :], tgt, one, ld, torch.ones_like(mass))
+    torch.testing.assert_close(new[..., 0, :], tgt, atol=1e-6, rtol=1e-5)
+    new = rows + torch_oracle.proposal_delta(rows, w, pred, tgt, torch.zeros_like(beta), ld, torch.ones_like(mass))
+    torch.testing.assert_close(new, ld.exp()[..., None] * rows, atol=1e-6, rtol=1e-5)
+    zero = torch_oracle.proposal_delta(rows, w, pred, tgt, beta, ld, torch.zeros_like(mass))
+    assert zero.abs().max().item() == 0.0
