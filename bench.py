@@ -11,6 +11,11 @@ factor scores per head), key dim dk=128, value dim D=128 (H*D = 1024), top-k
 (score+route is one fused kernel: MFMA scores feed the top-k through LDS)
 
 with the bank updated in place at every 512-token clock (donated commit).
+``--write-path proposals`` replaces the synthetic deltas by the stack's write
+path (S/layers/global_layer.py:42-54): routed read of the write route
+(prediction) -> proposal error terms -> fused proposal commit, whose deltas
+are formed inside the commit; ``proposals-materialised`` runs the same work
+the reference's way (gather rows -> materialised fp32 deltas -> commit).
 Inputs are synthetic, generated on the CPU with a seeded generator and copied
 to HBM before the timed region.  Prints one JSON line (see the driver
 contract); rank 0 only, one GPU.
@@ -87,6 +92,24 @@ def make_inputs(cfg, seed=0):
     return keys.bfloat16(), bank, qr.bfloat16(), qw.bfloat16(), delta
 
 
+WRITE_PATHS = {
+    "deltas": "commit of synthetic deltas",
+    "proposals": "write read + proposal error + fused proposal commit",
+    "proposals-materialised": "write read + row gather + proposal deltas + commit",
+}
+
+
+def make_write_operands(cfg, seed=1):
+    """Value targets (config dtype), gates beta/log_decay [B, T, H, 1] (as
+    S/layers/global_layer.py:47-49 forms them) for the proposal write path."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    B, T, H, D = (cfg[x] for x in ("B", "T", "H", "D"))
+    target = (torch.randn(B, T, H, D, generator=g) * 0.1).to(cfg["dtype"])
+    beta = torch.randn(B, T, H, 1, generator=g).sigmoid()
+    log_decay = -torch.nn.functional.softplus(torch.randn(B, T, H, 1, generator=g) - 4)
+    return target, beta, log_decay
+
+
 class Pipeline:
     """Preallocated buffers and direct C-ABI calls for the 4-epoch workload.
 
@@ -102,9 +125,9 @@ class Pipeline:
       durations stop being a clean roofline measurement), so it is not the default.
     """
 
-    def __init__(self, cfg, device):
+    def __init__(self, cfg, device, write_path="deltas"):
         from glsdm import _native as N
-        self.N, self.cfg, self.dev = N, cfg, device
+        self.N, self.cfg, self.dev, self.write_path = N, cfg, device, write_path
         keys, bank, qr, qw, delta = make_inputs(cfg)
         B, T, C, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "C", "H", "half", "dk", "D", "k"))
         self.epochs = T // C
@@ -123,6 +146,17 @@ class Pipeline:
         N.call("glsdm_commit_workspace_bytes", self.E, self.rows, ctypes.byref(size))
         self.ws = torch.empty(size.value, dtype=torch.uint8, device=device)
         self.unique = torch.zeros(1, dtype=torch.int64, device=device)
+        if write_path != "deltas":
+            self.delta = None
+            target, beta, log_decay = make_write_operands(cfg)
+            self.target, self.beta, self.log_decay = split(target), split(beta), split(log_decay)
+            self.pred = torch.empty(B, C, H, D, dtype=torch.float32, device=device)
+            self.error = torch.empty(B, C, H, D, dtype=torch.float32, device=device)
+            self.decay = torch.empty(B, C, H, dtype=torch.float32, device=device)
+            self.mass = torch.ones(B, C, dtype=torch.float32, device=device)
+            if write_path == "proposals-materialised":
+                self.rows_buf = torch.empty(B, C, H, k, D, dtype=self.bank.dtype, device=device)
+                self.dbuf = torch.empty(B, C, H, k, D, dtype=torch.float32, device=device)
         self.mem_stream = torch.cuda.current_stream(device)
         self.route_stream = torch.cuda.Stream(device)          # default priority
         self.routed = [torch.cuda.Event() for _ in range(self.epochs)]
@@ -158,13 +192,38 @@ class Pipeline:
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, D, k = (c[x] for x in ("B", "C", "H", "half", "D", "k"))
         dt = N.dtype_code(self.bank)
+        uq = p(self.unique) if count_unique else None
         self._timed("read", stream, lambda: N.call(
             "glsdm_read", p(self.bank), dt, B, H, half * half, D, C, k, p(self.idx[e]), p(self.w[e]),
             p(self.out), N.F32, st))
+        if self.write_path == "deltas":
+            self._timed("commit", stream, lambda: N.call(
+                "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.delta[e]), dt,
+                p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(), uq, st))
+            return
+        R = B * C * H
+        # the write route's routed read: the proposal's prediction
+        self._timed("write_read", stream, lambda: N.call(
+            "glsdm_read", p(self.bank), dt, B, H, half * half, D, C, k, p(self.widx[e]), p(self.ww[e]),
+            p(self.pred), N.F32, st))
+        if self.write_path == "proposals":
+            self._timed("proposal_error", stream, lambda: N.call(
+                "glsdm_proposal_error", R, D, p(self.pred), p(self.target[e]), N.dtype_code(self.target[e]),
+                p(self.beta[e]), p(self.log_decay[e]), p(self.error), p(self.decay), st))
+            self._timed("commit", stream, lambda: N.call(
+                "glsdm_commit_proposals", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.ckeys[e]),
+                self.E, k, p(self.ww[e]), p(self.error), p(self.decay), p(self.mass), H, p(self.ws),
+                self.ws.numel(), uq, st))
+            return
+        self._timed("gather", stream, lambda: N.call(
+            "glsdm_gather_rows", p(self.bank), dt, self.rows, D, p(self.addr[e]), self.E, p(self.rows_buf), st))
+        self._timed("proposal_delta", stream, lambda: N.call(
+            "glsdm_proposal_delta", p(self.rows_buf), dt, R, k, D, p(self.ww[e]), p(self.pred),
+            p(self.target[e]), N.dtype_code(self.target[e]), p(self.beta[e]), p(self.log_decay[e]),
+            p(self.mass), H, p(self.dbuf), st))
         self._timed("commit", stream, lambda: N.call(
-            "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.delta[e]), dt,
-            p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(),
-            p(self.unique) if count_unique else None, st))
+            "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.dbuf), N.F32,
+            p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(), uq, st))
 
     def step_serial(self):
         for e in range(self.epochs):
@@ -197,16 +256,31 @@ class Pipeline:
         return out
 
 
-def algorithmic_bytes(cfg, unique):
-    """Read + commit HBM bytes per epoch (queries bf16; bank and deltas in the config's dtype)."""
+def algorithmic_bytes(cfg, unique, write_path="deltas"):
+    """HBM bytes per epoch: (read incl. queries, read kernel, [commit launch per
+    epoch], other write-path work).  Bank and deltas in the config's dtype.
+
+    ``deltas``: the commit reads the synthetic deltas, addresses and keys and
+    each touched row twice.  Proposal write paths add the write route's read
+    (k rows, fp32 prediction, index/weights) and the error terms' inputs
+    (prediction fp32, target, gates) as other work; their commit launch reads
+    each error row and decay/mass once plus weight, address and key per entry
+    (``proposals``), or the materialised fp32 deltas, addresses and keys
+    (``proposals-materialised``: the gather and delta kernels are that
+    path's own overhead and are not counted as algorithmic)."""
     B, C, H, dk, D, k = (cfg[x] for x in ("B", "C", "H", "dk", "D", "k"))
     sv = torch.tensor([], dtype=cfg["dtype"]).element_size()
     rows = B * C * H
     read_kernel = rows * (k * D * sv + D * 4 + k * 12)           # gathers + fp32 out + idx/w
     read = read_kernel + rows * dk * 2                            # + queries read once
     E = rows * k
-    commit = [E * D * sv + E * 16 + 2 * u * D * sv for u in unique]
-    return read, read_kernel, commit
+    rmw = [2 * u * D * sv for u in unique]
+    if write_path == "deltas":
+        return read, read_kernel, [E * D * sv + E * 16 + x for x in rmw], 0
+    other = read_kernel + rows * (D * 4 + D * sv + 12)
+    if write_path == "proposals":
+        return read, read_kernel, [rows * (D * 4 + 8) + E * 20 + x for x in rmw], other
+    return read, read_kernel, [E * D * 4 + E * 16 + x for x in rmw], other
 
 
 def cpu_baseline(cfg, budget_s=12.0):
@@ -255,6 +329,10 @@ def main():
     ap.add_argument("--compare-schedules", action="store_true",
                     help="also time the other schedule (reported as ms_per_step_other_schedule)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--write-path", choices=("deltas", "proposals", "proposals-materialised"), default="deltas",
+                    help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
+                         "path with the fused proposal commit; proposals-materialised: the same work with "
+                         "gathered rows and stored fp32 deltas")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed region, copy 256 MiB device-to-device 3 times (a kernel of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -268,7 +346,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
-    pipe = Pipeline(cfg, dev)
+    pipe = Pipeline(cfg, dev, args.write_path)
     unique = pipe.unique_rows()
     for _ in range(args.warmup):
         pipe.step()
@@ -324,9 +402,9 @@ def main():
     calls = {n: len(v) // 3 for n, v in pipe.timers.items()}
 
     tokens = cfg["B"] * cfg["T"]
-    read_b, read_kernel_b, commit_b = algorithmic_bytes(cfg, unique)
+    read_b, read_kernel_b, commit_b, other_b = algorithmic_bytes(cfg, unique, args.write_path)
     epochs = pipe.epochs
-    alg_total = epochs * read_b + sum(commit_b)
+    alg_total = epochs * (read_b + other_b) + sum(commit_b)
     # dominant call: largest share of step time
     per_call[dominant] = dominant_ms[dominant]     # measured inside the timed region
     if dominant == "read":
@@ -335,7 +413,8 @@ def main():
         achieved = bytes_launch / t_launch / 1e9
     elif dominant == "commit":
         bytes_launch, t_launch = statistics.mean(commit_b), per_call["commit"] * 1e-3
-        roof = {"kernel": "glsdm_commit (pack + radix passes + segment)", "bound": "hbm", "unit": "GB/s",
+        entry = "glsdm_commit_proposals" if args.write_path == "proposals" else "glsdm_commit"
+        roof = {"kernel": f"{entry} (pack + radix passes + segment)", "bound": "hbm", "unit": "GB/s",
                 "peak": HBM_PEAK / 1e9}
         achieved = bytes_launch / t_launch / 1e9
     else:
@@ -346,12 +425,13 @@ def main():
                 "peak": MFMA_BF16_PEAK / 1e12}
         achieved = flops / t_launch / 1e12
         bytes_launch = None
-    traffic = TRAFFIC_PER_LAUNCH.get(dominant) if args.config == 2 else None
+    traffic = TRAFFIC_PER_LAUNCH.get(dominant) if args.config == 2 and args.write_path == "deltas" else None
     roof.update({"achieved": round(achieved, 1), "frac": round(achieved / roof["peak"], 4),
                  "traffic": None if traffic is None else int(traffic)})
 
     scoring_flops = 2 * cfg["B"] * cfg["C"] * cfg["H"] * 2 * cfg["half"] * cfg["dk"]
-    rc_time = epochs * (per_call["read"] + per_call["commit"]) * 1e-3
+    memory_calls = ("read", "commit", "write_read", "proposal_error", "gather", "proposal_delta")
+    rc_time = sum(per_call[n] * calls[n] for n in memory_calls if n in per_call) * 1e-3
     result = {
         "metric": "GL-SDM mem-op tokens/s + % HBM roofline (read+commit); full-stack tokens/s",
         "value": round(tokens / (ms_step * 1e-3), 1),
@@ -371,10 +451,10 @@ def main():
                                f"({epochs} epochs of {cfg['C']}) H={cfg['H']} M={cfg['half'] ** 2} dk={cfg['dk']} "
                                f"D={cfg['D']} k={cfg['k']} {'bf16' if cfg['dtype'] == torch.bfloat16 else 'fp32'}"
                                f"{' Zipf-skewed' if cfg['skew'] else ''}, fused score-route + read + fused "
-                               "score-route + keys + commit",
+                               "score-route + keys + " + WRITE_PATHS[args.write_path],
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
                    "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
-                   "parallelism": "single GPU"},
+                   "write_path": args.write_path, "parallelism": "single GPU"},
         "roofline": roof,
         "read_commit_hbm": {"bytes_per_step": alg_total, "seconds_per_step": rc_time,
                             "achieved_GBps": round(alg_total / rc_time / 1e9, 1),

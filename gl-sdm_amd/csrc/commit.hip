@@ -53,6 +53,9 @@ constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // 512 consecutive entries per wave
 constexpr int MAX_PASSES = 8;
 constexpr int64_t MAX_ENTRIES = (int64_t)1 << 30;       // look-back words hold 30-bit counts
+#ifndef GLSDM_SEG_WAVES
+#define GLSDM_SEG_WAVES 8192                             // segment waves wanted before windows shrink
+#endif
 
 constexpr uint32_t LB_AGGREGATE = 1u << 30;             // tile's own count published
 constexpr uint32_t LB_PREFIX = 2u << 30;                // inclusive prefix published
@@ -281,21 +284,23 @@ struct ProposalTerms {
     }
 };
 
-// One wavefront per 64 consecutive sorted positions; lane groups of `lpr` lanes
-// (one bank row each) walk the address runs that start in the wave's window.
+// One wavefront per window of `win` (a power of two <= 64) consecutive sorted
+// positions; lane groups of `lpr` lanes (one bank row each) walk the address
+// runs that start in the window, continuing past its end when a run does.
 template <typename TB, typename SRC, int VEC, int CH>
 __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int64_t rows, int64_t D,
                                                       const int64_t *__restrict__ keys, const SRC src,
                                                       const uint64_t *__restrict__ sorted, int64_t n, int ebits,
-                                                      int nv, int lpr, unsigned long long *__restrict__ unique_out)
+                                                      int nv, int lpr, int win,
+                                                      unsigned long long *__restrict__ unique_out)
 {
 #pragma clang fp contract(off)
     __shared__ uint64_t s_w[4][64];
     __shared__ int s_head[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * 64;
+    const int64_t p0 = ((int64_t)blockIdx.x * 4 + wave) * win;
     const int64_t p = p0 + lane;
-    const bool valid = p < n;
+    const bool valid = lane < win && p < n;
     const uint64_t emask = (1ull << ebits) - 1ull;
     const uint64_t w = valid ? sorted[p] : ~0ull;
     const int64_t a = valid ? (int64_t)(w >> ebits) : -1;
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
 
     const int ng = 64 / lpr;
     const int grp = lane / lpr, li = lane % lpr;
-    auto word_at = [&](int q) -> uint64_t { return q < 64 ? s_w[wave][q] : sorted[p0 + q]; };
+    auto word_at = [&](int q) -> uint64_t { return q < win ? s_w[wave][q] : sorted[p0 + q]; };
     auto add_delta = [&](int64_t ent, const float (&old)[CH][VEC], float (&acc)[CH][VEC]) {
         if (ent >= n) return;                           // impossible after a correct sort; never read out of bounds
         const typename SRC::Entry e = src.entry(ent);
@@ -348,19 +353,22 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
             }
             if (v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
         }
-        // arrival order is key order unless a later entry has a smaller key
+        // arrival order is key order unless a later entry has a smaller key; the
+        // group's lanes compare the run's neighbouring pairs in parallel
         bool in_order = true;
         auto key_of = [&](uint64_t word) -> int64_t {
             const int64_t e = (int64_t)(word & emask);
             return e < n ? keys[e] : INT64_MAX;
         };
         if (keys && len > 1) {
-            int64_t k0 = key_of(hw);
-            for (int q = 1; q < len && in_order; ++q) {
-                const int64_t k1 = key_of(word_at(h + q));
-                in_order = k1 >= k0;
-                k0 = k1;
+            bool ok = true;
+            for (int q = 1 + li; q < len; q += lpr) {
+                const int64_t k0 = key_of(word_at(h + q - 1)), k1 = key_of(word_at(h + q));
+                ok &= k1 >= k0;
             }
+            const uint64_t bad = __ballot(!ok);
+            const uint64_t mine = (lpr >= 64 ? ~0ull : ((1ull << lpr) - 1ull)) << (grp * lpr);
+            in_order = (bad & mine) == 0;
         }
         if (in_order) {
             for (int q = 0; q < len; ++q) add_delta((int64_t)(word_at(h + q) & emask), old, acc);
@@ -399,12 +407,18 @@ static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t 
                              const uint64_t *sorted, int64_t n, int ebits, const RowPlan &p,
                              int64_t *unique_out, hipStream_t st)
 {
-    const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
+    // window: 64 positions per wave when that still makes GLSDM_SEG_WAVES waves,
+    // shorter for small commits (so they fill the chip), never below one
+    // position per lane group
+    const int groups = 64 / p.lpr;
+    int win = 64;
+    while (win > groups && ceil_div(n, win) < GLSDM_SEG_WAVES) win >>= 1;
+    const dim3 grid((unsigned)ceil_div(n, 4 * win)), block(256);
     TB *bk = static_cast<TB *>(bank);
     auto *u = reinterpret_cast<unsigned long long *>(unique_out);
 #define GLSDM_SEG_LAUNCH(C)                                                                                    \
     hipLaunchKernelGGL((segment_kernel<TB, SRC, VEC, C>), grid, block, 0, st, bk, rows, D, keys, src, sorted, n, \
-                       ebits, p.nv, p.lpr, u)
+                       ebits, p.nv, p.lpr, win, u)
     switch (p.ch) {
     case 1: GLSDM_SEG_LAUNCH(1); break;
     case 2: GLSDM_SEG_LAUNCH(2); break;
