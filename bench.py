@@ -145,6 +145,9 @@ class Pipeline:
         size = ctypes.c_size_t(0)
         N.call("glsdm_commit_workspace_bytes", self.E, self.rows, ctypes.byref(size))
         self.ws = torch.empty(size.value, dtype=torch.uint8, device=device)
+        N.call("glsdm_score_route_workspace_bytes", B, C, H, half, k, ctypes.byref(size))
+        # one route workspace: both routing calls of an epoch run on the same stream, one after the other
+        self.route_ws = torch.empty(max(size.value, 8), dtype=torch.uint8, device=device)
         self.unique = torch.zeros(1, dtype=torch.int64, device=device)
         if write_path != "deltas":
             self.delta = None
@@ -180,10 +183,10 @@ class Pipeline:
         B, C, H, half, dk, k = (c[x] for x in ("B", "C", "H", "half", "dk", "k"))
         self._timed("score_route", stream, lambda: N.call(
             "glsdm_score_route", p(self.qr[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, None,
-            p(self.idx[e]), p(self.w[e]), st))
+            p(self.idx[e]), p(self.w[e]), p(self.route_ws), self.route_ws.numel(), st))
         self._timed("score_route", stream, lambda: N.call(
             "glsdm_score_route", p(self.qw[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, None,
-            p(self.widx[e]), p(self.ww[e]), st))
+            p(self.widx[e]), p(self.ww[e]), p(self.route_ws), self.route_ws.numel(), st))
         self._timed("keys", stream, lambda: N.call(
             "glsdm_proposal_keys", p(self.widx[e]), B, C, H, k, half * half, 0, C, 1, 0,
             p(self.addr[e]), p(self.ckeys[e]), st))

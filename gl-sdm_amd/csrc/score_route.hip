@@ -12,6 +12,13 @@
 // head-fastest, so with 8 heads on 8 XCDs each XCD's L2 serves one head's
 // sub-key table.
 //
+// Split path, for launches that would leave most CUs idle (few tokens, one
+// head): score_part_kernel blocks each own one factor and one range of its
+// sub-key columns for R tokens and write that range's exact top-K keys to a
+// caller workspace; route_merge_kernel merges a token's per-range lists into
+// the factor lists (exact: each range list holds its range's K best, K >= kk)
+// and runs the candidate stage and softmax.  Same results, bit for bit.
+//
 // Semantics: scores as glsdm_score, routing as glsdm_route (the chosen slots,
 // weights and tie rule are identical on identical scores).
 #include "select.h"
@@ -194,6 +201,212 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     finish_route<K, G>(t, width, tie, g, live, index + out_row * width, weights + out_row * width);
 }
 
+// One block: R tokens of head h, factor f, sub-key columns [s*span, s*span + span).
+template <int K, int G, int CW, int KSM, bool STAGE>
+__global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restrict__ q,
+                                                         const bf16_t *__restrict__ keys, int64_t N, int64_t H,
+                                                         int dk, int half, int tie, int splits, int span,
+                                                         float *__restrict__ scores_out,
+                                                         uint64_t *__restrict__ parts)
+{
+    constexpr int R = 256 / G;
+    constexpr int RT = R / 16;
+    constexpr int WPR = 4 / RT;
+    constexpr int CT = CW / 16;
+    constexpr int CTW = CT / WPR;
+    constexpr int SUB = CW / (G * K);
+    constexpr int LDW = CW + 4;
+    constexpr int LDK = KSM * 32 + 8;
+    constexpr int VPR = KSM * 4;
+    constexpr int PIECES = (CW * VPR + 255) / 256;
+    constexpr int SKC = STAGE ? CW : 1, SKL = STAGE ? LDK : 8;
+    constexpr bool WAVE_LOCAL = (RT == 4 && WPR == 1 && G == 4);
+    static_assert(RT >= 1 && RT <= 4 && CT % WPR == 0 && CTW >= 1 && SUB >= 1, "tiling");
+    __shared__ __attribute__((aligned(16))) float s_sc[R][LDW];
+    __shared__ __attribute__((aligned(16))) bf16_t s_k[SKC][SKL];
+
+    // block order: head fastest, then column range, factor, token tile
+    int64_t bid = blockIdx.x;
+    const int h = (int)(bid % H);
+    bid /= H;
+    const int s = (int)(bid % splits);
+    bid /= splits;
+    const int f = (int)(bid % 2);
+    const int64_t n0 = (bid / 2) * R;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rt = wave % RT, cshare = wave / RT;
+    const int li = lane & 15, kq = lane >> 4;
+    const int L = 2 * half;
+    const int ks = dk / 32;
+    const int vpr = dk / 8;
+    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int64_t row_n = n0 + lr;
+    const int lo = s * span, hi = min(half, lo + span);
+
+    int64_t qn = n0 + rt * 16 + li;
+    if (qn >= N) qn = N - 1;
+    const bf16_t *qrow = q + (qn * H + h) * dk + kq * 8;
+    bf16x8_t qa[KSM];
+#pragma unroll
+    for (int t = 0; t < KSM; ++t)
+        if (t < ks) qa[t] = *reinterpret_cast<const bf16x8_t *>(qrow + t * 32);
+    const bf16_t *fkeys = keys + ((int64_t)h * L + (int64_t)f * half) * dk;
+
+    uint64_t ta[K];
+    list_clear<K>(ta);
+    for (int c0 = lo; c0 < hi; c0 += CW) {
+        if constexpr (STAGE) {
+            __syncthreads();                  // every wavefront is done with the previous s_k
+#pragma unroll
+            for (int p = 0; p < PIECES; ++p) {
+                const int id = threadIdx.x + 256 * p;
+                const int col = id / vpr, sl = id - col * vpr;
+                if (col < CW && c0 + col < half)
+                    *reinterpret_cast<uint4 *>(&s_k[col][sl * 8]) =
+                        *reinterpret_cast<const uint4 *>(fkeys + (int64_t)(c0 + col) * dk + sl * 8);
+            }
+            __syncthreads();                  // s_k holds this chunk
+        }
+#pragma unroll
+        for (int j = 0; j < CTW; ++j) {
+            const int ct = cshare * CTW + j;
+            const int col = c0 + ct * 16;
+            if (col >= half) continue;        // wave-uniform: half % 16 == 0
+            const bf16_t *krow = STAGE ? &s_k[ct * 16 + li][kq * 8] : fkeys + (int64_t)(col + li) * dk + kq * 8;
+            floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < KSM; ++t)
+                if (t < ks)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        qa[t], *reinterpret_cast<const bf16x8_t *>(krow + t * 32), acc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s_sc[rt * 16 + 4 * kq + r][ct * 16 + li] = acc[r];
+            if (scores_out) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t n = n0 + rt * 16 + 4 * kq + r;
+                    if (n < N) scores_out[(n * H + h) * L + f * half + col + li] = acc[r];
+                }
+            }
+        }
+        chunk_sync<WAVE_LOCAL>();
+#pragma unroll
+        for (int sub = 0; sub < SUB; ++sub) {
+            const int first = (sub * G + g) * K;
+            uint64_t a[K];
+#pragma unroll
+            for (int qi = 0; qi < K; ++qi) {
+                const int col = c0 + first + qi;
+                a[qi] = col < hi ? rank_key(s_sc[lr][first + qi], (uint32_t)col, tie) : 0;
+            }
+            list_absorb<K>(ta, a);
+        }
+        chunk_sync<WAVE_LOCAL>();
+    }
+    group_merge<K, G>(ta);
+    if (row_n < N) {
+        uint64_t *out = parts + (((row_n * H + h) * 2 + f) * splits + s) * K;
+#pragma unroll
+        for (int w = 0; w < K; ++w)
+            if (w % G == g) out[w] = ta[w];
+    }
+}
+
+// One G-lane group per token-head row: merge the per-range lists of each factor,
+// then the candidate stage and the softmax as in score_route_kernel.
+template <int K, int G>
+__global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__restrict__ parts, int64_t rows,
+                                                          int splits, int half, int width, int tie,
+                                                          int64_t *__restrict__ index, float *__restrict__ weights)
+{
+    constexpr int RPB = 256 / G;
+    __shared__ uint32_t s_idx[RPB][2][K];
+    __shared__ float s_val[RPB][2][K];
+    __shared__ uint16_t s_pairs[STAIR_MAX];
+    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;
+    const int kk = width < half ? width : half;
+    const int npairs = staircase_build(s_pairs, kk, width);
+    bool finite = true;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        uint64_t t[K];
+        list_clear<K>(t);
+        for (int s = g; s < splits; s += G) {
+            const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
+            uint64_t c[K];
+#pragma unroll
+            for (int w = 0; w < K; ++w) c[w] = src[w];
+            merge_top<K>(t, c);
+        }
+        group_merge<K, G>(t);
+        const bool ok = stash_factor<K, G>(t, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
+        finite = finite && ok;
+    }
+    __syncthreads();
+    uint64_t t[K];
+    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
+                        npairs, finite, t);
+    finish_route<K, G>(t, width, tie, g, live, index + r * width, weights + r * width);
+}
+
+// The split path's shape for (N, H, half, width): 0 splits when the single
+// kernel already fills the GPU (or the split path would not add blocks).
+struct SplitPlan {
+    int splits, span, cw, r;
+    size_t bytes;
+};
+
+constexpr int64_t SPLIT_MIN_BLOCKS = 256;    // single-kernel launches below one block per CU split
+constexpr int64_t SPLIT_TARGET_BLOCKS = 512;
+
+static SplitPlan split_plan(int64_t N, int64_t H, int half, int width)
+{
+    SplitPlan p{0, 0, 0, 0, 0};
+    const int K = pow2_ceil(width);
+    const int r_single = K >= 32 ? 32 : 64;   // tokens per block of score_route_kernel (G = 8 for K >= 32)
+    if (ceil_div(N, r_single) * H >= SPLIT_MIN_BLOCKS) return p;
+    p.cw = K <= 16 ? 64 : 4 * K;              // G = 4 lanes per token, K columns per lane and chunk
+    p.r = 64;
+    const int chunks = (int)ceil_div(half, p.cw);
+    const int64_t tiles = ceil_div(N, p.r) * H * 2;
+    int splits = 1;
+    while (splits < chunks && tiles * splits < SPLIT_TARGET_BLOCKS) splits <<= 1;
+    if (splits > chunks) splits = chunks;
+    p.splits = splits;
+    p.span = (int)ceil_div(chunks, splits) * p.cw;
+    p.bytes = (size_t)N * (size_t)H * 2 * (size_t)splits * (size_t)K * sizeof(uint64_t);
+    return p;
+}
+
+template <int K>
+static int launch_split(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half, int width,
+                        int tie, const SplitPlan &p, float *scores_out, uint64_t *parts, int64_t *index,
+                        float *weights, hipStream_t st)
+{
+    constexpr int G = 4;
+    constexpr int CW = K <= 16 ? 64 : 4 * K;
+    constexpr bool STAGE = K <= 16;
+    const int64_t blocks = ceil_div(N, 256 / G) * H * 2 * p.splits;
+    if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: grid too large");
+    const bf16_t *qq = static_cast<const bf16_t *>(q), *kk = static_cast<const bf16_t *>(keys);
+    if (dk <= 128)
+        hipLaunchKernelGGL((score_part_kernel<K, G, CW, 4, STAGE>), dim3((unsigned)blocks), dim3(256), 0, st, qq,
+                           kk, N, H, dk, half, tie, p.splits, p.span, scores_out, parts);
+    else
+        hipLaunchKernelGGL((score_part_kernel<K, G, CW, KS_MAX, STAGE>), dim3((unsigned)blocks), dim3(256), 0, st,
+                           qq, kk, N, H, dk, half, tie, p.splits, p.span, scores_out, parts);
+    int rc = check_launch("score_part_kernel");
+    if (rc) return rc;
+    constexpr int MG = K >= 32 ? 8 : 4;
+    const int64_t rows = N * H;
+    hipLaunchKernelGGL((route_merge_kernel<K, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0, st,
+                       parts, rows, p.splits, half, width, tie, index, weights);
+    return check_launch("route_merge_kernel");
+}
+
 template <int K, int G, int CW, bool PAIR>
 static int launch_score_route(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half,
                               int width, int tie, float *scores_out, int64_t *index, float *weights,
@@ -217,9 +430,20 @@ static int launch_score_route(const void *q, const void *keys, int64_t N, int64_
 
 using namespace glsdm;
 
+extern "C" int glsdm_score_route_workspace_bytes(int64_t B, int64_t T, int64_t H, int32_t half, int32_t width,
+                                                 size_t *bytes)
+{
+    if (!bytes) return fail(GLSDM_ERR_ARG, "score_route_workspace_bytes: null output");
+    if (B < 0 || T < 0 || H < 1 || half < 1 || width < 1 || width > 64)
+        return fail(GLSDM_ERR_ARG, "score_route_workspace_bytes: bad shape");
+    *bytes = B * T == 0 ? 0 : split_plan(B * T, H, half, width).bytes;
+    return GLSDM_OK;
+}
+
 extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
                                  int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
-                                 int64_t *index, float *weights, void *stream)
+                                 int64_t *index, float *weights, void *workspace, size_t workspace_bytes,
+                                 void *stream)
 {
     if (B < 0 || T < 0 || H < 1 || dk < 1 || half < 1) return fail(GLSDM_ERR_ARG, "score_route: bad shape");
     if (dk % 32 != 0 || dk > 32 * KS_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: dk=%d must be a multiple of 32 up to 256", dk);
@@ -233,6 +457,20 @@ extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64
     if (((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(subkeys)) & 15) != 0)
         return fail(GLSDM_ERR_UNSUPPORTED, "score_route: queries and sub-keys must be 16-byte aligned");
     const hipStream_t st = as_stream(stream);
+    const SplitPlan plan = split_plan(N, H, half, width);
+    if (plan.splits > 0 && workspace && workspace_bytes >= plan.bytes &&
+        (reinterpret_cast<uintptr_t>(workspace) & 7) == 0) {
+        uint64_t *parts = static_cast<uint64_t *>(workspace);
+        switch (pow2_ceil(width)) {
+        case 1: return launch_split<1>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 2: return launch_split<2>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 4: return launch_split<4>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 8: return launch_split<8>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 16: return launch_split<16>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 32: return launch_split<32>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        default: return launch_split<64>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        }
+    }
     switch (pow2_ceil(width)) {
     case 1: return launch_score_route<1, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
     case 2: return launch_score_route<2, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);

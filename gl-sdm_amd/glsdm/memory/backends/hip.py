@@ -122,9 +122,19 @@ def score(queries, subkeys):
     return out
 
 
-def score_route(queries, subkeys, width, tie="highest", export_scores=False):
+def score_route_workspace_bytes(B, T, H, half, width):
+    size = N.ctypes.c_size_t(0)
+    N.call("glsdm_score_route_workspace_bytes", B, T, H, half, width, N.ctypes.byref(size))
+    return size.value
+
+
+def score_route(queries, subkeys, width, tie="highest", export_scores=False, split=True, workspace=None):
     """Fused MFMA scoring + route: bf16 queries ``[B,T,H,dk]`` and sub-keys ``[H,L,dk]``
-    -> ``(index int64 [B,T,H,width], weights fp32, scores fp32 [B,T,H,L] or None)``."""
+    -> ``(index int64 [B,T,H,width], weights fp32, scores fp32 [B,T,H,L] or None)``.
+
+    ``split`` lets small launches (few tokens, one head) spread each factor's
+    sub-key columns over more blocks through a workspace (``workspace``, uint8
+    device tensor, allocated here when not given); results are identical either way."""
     _no_grad(queries, subkeys)
     device = require_cuda(queries, subkeys)
     if queries.dtype != torch.bfloat16 or subkeys.dtype != torch.bfloat16:
@@ -139,8 +149,13 @@ def score_route(queries, subkeys, width, tie="highest", export_scores=False):
     index = torch.empty((B, T, H, width), dtype=torch.int64, device=device)
     weights = torch.empty((B, T, H, width), dtype=torch.float32, device=device)
     scores = torch.empty((B, T, H, L), dtype=torch.float32, device=device) if export_scores else None
+    need = score_route_workspace_bytes(B, T, H, half, width) if split else 0
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    ws = workspace if need else None
     N.call("glsdm_score_route", N.ptr(queries), N.ptr(subkeys), B, T, H, dk, half, width, N.TIES[tie],
-           N.ptr(scores), N.ptr(index), N.ptr(weights), N.stream(device))
+           N.ptr(scores), N.ptr(index), N.ptr(weights), N.ptr(ws), 0 if ws is None else ws.numel(),
+           N.stream(device))
     return index, weights, scores
 
 

@@ -107,6 +107,11 @@ int glsdm_score(const void *queries, const void *subkeys, int64_t B, int64_t T, 
  *   queries [B,T,H,dk] bf16, subkeys [H, 2*half, dk] bf16 (16-byte aligned)
  *   index [B,T,H,width] int64 out (ascending slots), weights fp32 out
  *   scores_out: NULL, or [B,T,H,2*half] fp32 to also export the scores
+ *   workspace: NULL, or glsdm_score_route_workspace_bytes() bytes (8-byte
+ *             aligned).  Launches with fewer token tiles than CUs (few
+ *             tokens, one head) then split every factor's sub-key columns
+ *             over more blocks and merge their exact partial top-k lists; the
+ *             results are the same, bit for bit, with or without it.
  * Results equal glsdm_route applied to the exported scores, bit for bit.
  * Envelope: dk a multiple of 32 up to 256, half a multiple of 16, width <= 64.
  * Replaces: S/layers/global_layer.py:26-27 and :42-43 (router.q/k projection
@@ -114,7 +119,16 @@ int glsdm_score(const void *queries, const void *subkeys, int64_t B, int64_t T, 
  */
 int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
                       int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
-                      int64_t *index, float *weights, void *stream);
+                      int64_t *index, float *weights, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/*
+ * Workspace bytes glsdm_score_route can use for this shape (0: the shape
+ * already fills the GPU and no workspace is used).  No counterpart in the
+ * reference (which materialises the [B,T,H,2*half] scores instead).
+ */
+int glsdm_score_route_workspace_bytes(int64_t B, int64_t T, int64_t H, int32_t half, int32_t width,
+                                      size_t *bytes);
 
 /*
  * Bytes of workspace glsdm_commit needs for `entries` deltas into a bank of

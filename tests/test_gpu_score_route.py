@@ -1,6 +1,8 @@
 """Fused MFMA scoring + route: the route is bit-exact against the oracle on the
 exported scores, the exported scores match a float64 contraction, and the
-result does not depend on whether scores are exported."""
+result does not depend on whether scores are exported, nor on whether small
+launches take the split path (per-range partial lists in a workspace, then a
+merge kernel) or the single kernel."""
 import pytest
 import torch
 
@@ -20,6 +22,7 @@ def _inputs(B, T, H, dk, half, seed, clusters=False):
     return q.bfloat16(), k.bfloat16()
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("tie", ["highest", "lowest"])
 @pytest.mark.parametrize("B,T,H,dk,half,width", [
     (8, 64, 8, 128, 256, 16),      # config 2 geometry
@@ -28,22 +31,23 @@ def _inputs(B, T, H, dk, half, seed, clusters=False):
     (2, 17, 2, 32, 16, 4), (1, 33, 3, 96, 48, 5), (1, 20, 1, 256, 32, 64), (1, 9, 2, 64, 16, 1),
     (1, 18, 2, 64, 32, 2), (1, 70, 1, 128, 512, 8),
 ])
-def test_fused_route_matches_oracle_on_exported_scores(device, tie, B, T, H, dk, half, width):
+def test_fused_route_matches_oracle_on_exported_scores(device, split, tie, B, T, H, dk, half, width):
     q, k = _inputs(B, T, H, dk, half, seed=B * T + half + width)
-    idx, w, scores = hip.score_route(q.to(device), k.to(device), width, tie, export_scores=True)
+    idx, w, scores = hip.score_route(q.to(device), k.to(device), width, tie, export_scores=True, split=split)
     ref = torch.einsum("bthe,hce->bthc", q.double(), k.double())
     torch.testing.assert_close(scores.cpu().double(), ref, atol=1e-5, rtol=1e-5)
     ridx, rw = c_oracle.route(scores.cpu(), width, tie)
     assert torch.equal(idx.cpu(), ridx)
     torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
-    idx2, w2, none = hip.score_route(q.to(device), k.to(device), width, tie)
+    idx2, w2, none = hip.score_route(q.to(device), k.to(device), width, tie, split=not split)
     assert none is None and torch.equal(idx2, idx) and torch.equal(w2, w)
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("tie", ["highest", "lowest"])
-def test_fused_route_with_duplicate_subkeys(device, tie):
+def test_fused_route_with_duplicate_subkeys(device, split, tie):
     q, k = _inputs(2, 64, 2, 64, 64, seed=5, clusters=True)
-    idx, w, scores = hip.score_route(q.to(device), k.to(device), 16, tie, export_scores=True)
+    idx, w, scores = hip.score_route(q.to(device), k.to(device), 16, tie, export_scores=True, split=split)
     ridx, rw = torch_oracle.route(scores.cpu(), 16, tie)
     assert torch.equal(idx.cpu(), ridx)
     torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
@@ -55,3 +59,22 @@ def test_fused_route_equals_unfused(device):
     s = hip.score(q.to(device), k.to(device))
     idx2, w2 = hip.route(s, 16, "highest")
     assert torch.equal(idx, idx2) and torch.equal(w, w2)
+
+
+def test_split_plan_uses_workspace_only_for_small_launches():
+    assert hip.score_route_workspace_bytes(8, 512, 8, 256, 16) == 0           # config 2: 512 blocks already
+    need = hip.score_route_workspace_bytes(4, 512, 1, 1024, 32)               # config 3: 64 blocks
+    assert need > 0 and need % (4 * 512 * 2 * 32 * 8) == 0
+
+
+@pytest.mark.parametrize("tie", ["highest", "lowest"])
+def test_split_route_config3_epoch(device, tie):
+    """A full config-3 epoch (B=4, 512 tokens, one head, 1024 sub-keys per factor,
+    k=32) on the split path equals the single kernel and the oracle."""
+    q, k = _inputs(4, 512, 1, 128, 1024, seed=31)
+    idx, w, scores = hip.score_route(q.to(device), k.to(device), 32, tie, export_scores=True)
+    idx1, w1, _ = hip.score_route(q.to(device), k.to(device), 32, tie, split=False)
+    assert torch.equal(idx, idx1) and torch.equal(w, w1)
+    ridx, rw = c_oracle.route(scores.cpu(), 32, tie)
+    assert torch.equal(idx.cpu(), ridx)
+    torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
