@@ -40,7 +40,10 @@ namespace glsdm {
 
 constexpr int RADIX_BITS = 8;
 constexpr int RADIX = 1 << RADIX_BITS;
-constexpr int SORT_THREADS = 256;
+#ifndef GLSDM_SORT_THREADS
+#define GLSDM_SORT_THREADS 512
+#endif
+constexpr int SORT_THREADS = GLSDM_SORT_THREADS;       // >= RADIX: threads below RADIX own one digit each
 #ifndef GLSDM_SORT_ITEMS
 #define GLSDM_SORT_ITEMS 8
 #endif
@@ -48,9 +51,9 @@ constexpr int SORT_THREADS = 256;
 #define GLSDM_PACK_BLOCKS 128
 #endif
 constexpr int SORT_ITEMS = GLSDM_SORT_ITEMS;            // per thread
-constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // 2048 entries
+constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // entries per tile
 constexpr int SORT_WAVES = SORT_THREADS / 64;
-constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // 512 consecutive entries per wave
+constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // consecutive entries per wave
 constexpr int MAX_PASSES = 8;
 constexpr int64_t MAX_ENTRIES = (int64_t)1 << 30;       // look-back words hold 30-bit counts
 #ifndef GLSDM_SEG_WAVES
@@ -135,6 +138,26 @@ __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restric
     }
 }
 
+// Inclusive prefix sum of one value per digit over the digit-owner threads
+// (tid < RADIX, whole wavefronts): shuffle scans within wavefronts, one block
+// barrier, then the earlier wavefronts' totals.  Every thread of the block
+// calls it (non-owners pass 0).
+__device__ __forceinline__ uint32_t digit_scan(uint32_t x, uint32_t *s_wave)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    if (tid < RADIX && lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    uint32_t add = 0;
+    if (tid < RADIX)
+        for (int w = 0; w < wave; ++w) add += s_wave[w];
+    return x + add;
+}
+
 __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *__restrict__ in,
                                                                 uint64_t *__restrict__ out, int64_t n, int shift,
                                                                 const uint32_t *__restrict__ ghist,
@@ -142,29 +165,24 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
                                                                 uint32_t *__restrict__ counter,
                                                                 uint32_t *__restrict__ error)
 {
+    static_assert(SORT_THREADS >= RADIX && SORT_THREADS % 64 == 0, "one thread per digit");
     __shared__ uint32_t cnt[SORT_WAVES][RADIX];
-    __shared__ uint32_t base[RADIX];
-    __shared__ uint32_t scan[RADIX];
+    __shared__ int32_t base[RADIX];           // global position of the tile's first item of each digit, minus
+                                              // that item's position in the tile's digit-ordered LDS copy
+    __shared__ uint32_t s_wsum[2][RADIX / 64];
+    __shared__ uint32_t lstart[RADIX];        // first LDS position of each digit in the tile
+    __shared__ uint64_t s_items[SORT_TILE];   // the tile's items in (digit, rank) order
     __shared__ uint32_t s_tile;
     const int tid = threadIdx.x;
+    const bool owner = tid < RADIX;           // thread `tid` owns digit `tid`
     if (tid == 0) s_tile = atomicAdd(counter, 1u);     // tile ids in the order tiles start
-#pragma unroll
-    for (int w = 0; w < SORT_WAVES; ++w) cnt[w][tid] = 0;
-    scan[tid] = ghist[tid];
-    __syncthreads();
+    for (int x = tid; x < SORT_WAVES * RADIX; x += SORT_THREADS) (&cnt[0][0])[x] = 0;
+    // exclusive prefix over digits of the global histogram
+    const uint32_t own = owner ? ghist[tid] : 0u;
+    const uint32_t digit_base = digit_scan(own, s_wsum[0]) - own;   // its barrier also publishes cnt, s_tile
     const int64_t tile = s_tile;
 
-    // exclusive prefix over digits of the global histogram (Hillis-Steele in LDS)
-    const uint32_t own = scan[tid];
-    for (int off = 1; off < RADIX; off <<= 1) {
-        const uint32_t x = tid >= off ? scan[tid - off] : 0u;
-        __syncthreads();
-        scan[tid] += x;
-        __syncthreads();
-    }
-    const uint32_t digit_base = scan[tid] - own;
-
-    // stable rank of each item within its wave's 512 consecutive entries
+    // stable rank of each item within its wave's WAVE_ITEMS consecutive entries
     const int wave = tid >> 6, lane = tid & 63;
     const uint64_t lt = (1ull << lane) - 1ull;
     const int64_t start = tile * SORT_TILE + (int64_t)wave * WAVE_ITEMS;
@@ -192,42 +210,64 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
     }
     __syncthreads();
 
-    // thread `tid` owns digit `tid`: wave prefix, tile total, look-back
+    // digit owners: wave prefix and tile total, published at once
     uint32_t total = 0;
-#pragma unroll
-    for (int w = 0; w < SORT_WAVES; ++w) {
-        const uint32_t x = cnt[w][tid];
-        cnt[w][tid] = total;
-        total += x;
-    }
     uint32_t *word = status + tile * RADIX + tid;
-    uint32_t prefix = 0;
-    if (tile == 0) {
-        __hip_atomic_store(word, LB_PREFIX | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-        __hip_atomic_store(word, LB_AGGREGATE | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t *look = word - RADIX;
-        uint32_t spins = 0;
-        for (;;) {
-            const uint32_t s = __hip_atomic_load(look, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((s & ~LB_VALUE) == 0) {               // predecessor not published yet
-                if (++spins > LB_SPIN_LIMIT) { atomicOr(error, 1u); break; }
-                continue;
-            }
-            prefix += s & LB_VALUE;
-            if (s & LB_PREFIX) break;
-            look -= RADIX;                             // aggregate only: keep walking back
+    if (owner) {
+#pragma unroll
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            const uint32_t x = cnt[w][tid];
+            cnt[w][tid] = total;
+            total += x;
         }
-        __hip_atomic_store(word, LB_PREFIX | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(word, (tile == 0 ? LB_PREFIX : LB_AGGREGATE) | total, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
-    base[tid] = digit_base + prefix;
-    __syncthreads();
 
+    // the tile's items in digit order in LDS: exclusive prefix of the tile totals
+    const uint32_t first = digit_scan(total, s_wsum[1]) - total;
+    if (owner) lstart[tid] = first;
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < SORT_ITEMS; ++k) {
         const int64_t i = start + k * 64 + lane;
-        const int64_t dst = (int64_t)base[dig[k]] + cnt[wave][dig[k]] + pos[k];
-        if (i < n && dst < n) out[dst] = v[k];   // dst < n always holds; the guard keeps a bug from faulting
+        const uint32_t at = lstart[dig[k]] + cnt[wave][dig[k]] + pos[k];
+        if (i < n && at < (uint32_t)SORT_TILE) s_items[at] = v[k];
+    }
+
+    // digit owners: decoupled look-back over earlier tiles' counts of their digit
+    if (owner) {
+        uint32_t prefix = 0;
+        if (tile > 0) {
+            const uint32_t *look = word - RADIX;
+            uint32_t spins = 0;
+            for (;;) {
+                const uint32_t s = __hip_atomic_load(look, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((s & ~LB_VALUE) == 0) {           // predecessor not published yet
+                    if (++spins > LB_SPIN_LIMIT) { atomicOr(error, 1u); break; }
+                    continue;
+                }
+                prefix += s & LB_VALUE;
+                if (s & LB_PREFIX) break;
+                look -= RADIX;                         // aggregate only: keep walking back
+            }
+            __hip_atomic_store(word, LB_PREFIX | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        base[tid] = (int32_t)(digit_base + prefix) - (int32_t)first;
+    }
+    __syncthreads();
+
+    // write-out in LDS order: consecutive threads write a digit's consecutive positions
+    const int64_t tile_n = n - tile * SORT_TILE;
+    const int valid_items = tile_n < SORT_TILE ? (int)tile_n : SORT_TILE;
+#pragma unroll
+    for (int k = 0; k < SORT_ITEMS; ++k) {
+        const int j = k * SORT_THREADS + tid;
+        if (j < valid_items) {
+            const uint64_t x = s_items[j];
+            const int64_t dst = (int64_t)base[(uint32_t)(x >> shift) & (RADIX - 1)] + j;
+            if (dst >= 0 && dst < n) out[dst] = x;   // always in range; the guard keeps a bug from faulting
+        }
     }
 }
 
