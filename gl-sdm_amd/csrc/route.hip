@@ -55,8 +55,13 @@ __global__ __launch_bounds__(256) void route_kernel(const float *__restrict__ sc
                 c0[q] = i < half ? rank_key(f0[i], (uint32_t)i, tie) : 0;
                 c1[q] = i < half ? rank_key(f1[i], (uint32_t)i, tie) : 0;
             }
-            list_absorb<K>(t0, c0);
-            list_absorb<K>(t1, c1);
+            if (base == 0) {
+                list_first<K>(t0, c0);
+                list_first<K>(t1, c1);
+            } else {
+                list_absorb<K>(t0, c0);
+                list_absorb<K>(t1, c1);
+            }
         }
         group_merge2<K, G>(t0, t1);
         const bool fa = stash_factor<K, G>(t0, kk, tie, g, s_idx[lr][0], s_val[lr][0]);

@@ -21,6 +21,8 @@
 //
 // Semantics: scores as glsdm_score, routing as glsdm_route (the chosen slots,
 // weights and tie rule are identical on identical scores).
+#include <type_traits>
+
 #include "select.h"
 
 namespace glsdm {
@@ -128,7 +130,10 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
         uint64_t ta[K], tb[K];
         list_clear<K>(ta);
         if constexpr (PAIR) list_clear<K>(tb);
-        for (int c0 = 0; c0 < half; c0 += CW) {
+        // one chunk of CW columns: MFMA scores into LDS, then each lane folds its share
+        // into its lists (the pass's first chunk becomes the lists: FIRST)
+        auto chunk = [&](int c0, auto first_tag) {
+            constexpr bool FIRST = decltype(first_tag)::value;
             if constexpr (STAGE) {
                 __syncthreads();                  // every wavefront is done with the previous s_k
                 stage_chunk(fp, c0);
@@ -175,11 +180,18 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
                     a[qi] = in ? rank_key(s_sc[0][lr][first + qi], (uint32_t)col, tie) : 0;
                     if constexpr (PAIR) b[qi] = in ? rank_key(s_sc[NF - 1][lr][first + qi], (uint32_t)col, tie) : 0;
                 }
-                list_absorb<K>(ta, a);
-                if constexpr (PAIR) list_absorb<K>(tb, b);
+                if (FIRST && sub == 0) {
+                    list_first<K>(ta, a);
+                    if constexpr (PAIR) list_first<K>(tb, b);
+                } else {
+                    list_absorb<K>(ta, a);
+                    if constexpr (PAIR) list_absorb<K>(tb, b);
+                }
             }
             chunk_sync<WAVE_LOCAL>();
-        }
+        };
+        chunk(0, std::true_type{});
+        for (int c0 = CW; c0 < half; c0 += CW) chunk(c0, std::false_type{});
         __syncthreads();   // the lists overwrite the score chunks of every wavefront
         if constexpr (PAIR) {
             group_merge2<K, G>(ta, tb);
@@ -254,7 +266,8 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
 
     uint64_t ta[K];
     list_clear<K>(ta);
-    for (int c0 = lo; c0 < hi; c0 += CW) {
+    auto chunk = [&](int c0, auto first_tag) {
+        constexpr bool FIRST = decltype(first_tag)::value;
         if constexpr (STAGE) {
             __syncthreads();                  // every wavefront is done with the previous s_k
 #pragma unroll
@@ -299,10 +312,15 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
                 const int col = c0 + first + qi;
                 a[qi] = col < hi ? rank_key(s_sc[lr][first + qi], (uint32_t)col, tie) : 0;
             }
-            list_absorb<K>(ta, a);
+            if (FIRST && sub == 0)
+                list_first<K>(ta, a);
+            else
+                list_absorb<K>(ta, a);
         }
         chunk_sync<WAVE_LOCAL>();
-    }
+    };
+    if (lo < hi) chunk(lo, std::true_type{});
+    for (int c0 = lo + CW; c0 < hi; c0 += CW) chunk(c0, std::false_type{});
     group_merge<K, G>(ta);
     if (row_n < N) {
         uint64_t *out = parts + (((row_n * H + h) * 2 + f) * splits + s) * K;

@@ -75,27 +75,45 @@ __device__ __forceinline__ void list_clear(uint64_t (&t)[K])
     for (int i = 0; i < K; ++i) t[i] = 0;
 }
 
-// Descending sort of 16 keys with the 60-comparator network (bitonic needs 80).
-__device__ __forceinline__ void sort16_desc(uint64_t (&v)[16])
+// Sort of 16 keys with the 60-comparator network (bitonic needs 80);
+// descending unless ASC.
+template <bool ASC = false>
+__device__ __forceinline__ void sort16(uint64_t (&v)[16])
 {
 #pragma unroll
     for (int c = 0; c < SORTNET16_SIZE; ++c) {
         const int i = SORTNET16[c][0], j = SORTNET16[c][1];
         const uint64_t a = v[i], b = v[j];
-        v[i] = a > b ? a : b;
-        v[j] = a > b ? b : a;
+        const bool up = ASC ? a < b : a > b;
+        v[i] = up ? a : b;
+        v[j] = up ? b : a;
     }
+}
+
+template <int K, bool DESC>
+__device__ __forceinline__ void chunk_sort(uint64_t (&c)[K])
+{
+    if constexpr (K == 16)
+        sort16<!DESC>(c);
+    else
+        bitonic_sort<K, DESC>(c);
 }
 
 // Merge one unsorted chunk of K keys into the lane's running list.
 template <int K>
 __device__ __forceinline__ void list_absorb(uint64_t (&t)[K], uint64_t (&c)[K])
 {
-    if constexpr (K == 16)
-        sort16_desc(c);
-    else
-        bitonic_sort<K, true>(c);
+    chunk_sort<K, true>(c);
     merge_top<K>(t, c);
+}
+
+// A lane's first chunk: sorted, it is the list (no merge with an empty list).
+template <int K>
+__device__ __forceinline__ void list_first(uint64_t (&t)[K], uint64_t (&c)[K])
+{
+    chunk_sort<K, true>(c);
+#pragma unroll
+    for (int i = 0; i < K; ++i) t[i] = c[i];
 }
 
 // Value of lane (lane ^ S) for S in {1, 2} through a DPP quad permute, else a shuffle.
@@ -154,7 +172,7 @@ __device__ __forceinline__ void group_merge2(uint64_t (&t)[K], uint64_t (&u)[K])
 template <int K, int G, typename KeyOf>
 __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (&t)[K])
 {
-    list_clear<K>(t);
+    if (n <= 0) list_clear<K>(t);
     for (int base = 0; base < n; base += G * K) {
         uint64_t c[K];
 #pragma unroll
@@ -162,7 +180,10 @@ __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (
             const int i = base + q * G + g;
             c[q] = i < n ? key_of(i) : 0;
         }
-        list_absorb<K>(t, c);
+        if (base == 0)
+            list_first<K>(t, c);
+        else
+            list_absorb<K>(t, c);
     }
     group_merge<K, G>(t);
 }
@@ -250,7 +271,7 @@ __device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, 
             u[w] = ~0ull;
         }
     }
-    bitonic_sort<K, false>(u);
+    chunk_sort<K, false>(u);
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < K; ++w) {
