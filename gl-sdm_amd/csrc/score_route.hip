@@ -351,8 +351,14 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
         uint64_t t[K];
-        list_clear<K>(t);
-        for (int s = g; s < splits; s += G) {
+        if (g < splits) {
+            const uint64_t *src = parts + ((r * 2 + f) * splits + g) * K;
+#pragma unroll
+            for (int w = 0; w < K; ++w) t[w] = src[w];
+        } else {
+            list_clear<K>(t);
+        }
+        for (int s = g + G; s < splits; s += G) {
             const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
             uint64_t c[K];
 #pragma unroll

@@ -172,6 +172,22 @@ __device__ __forceinline__ void group_merge2(uint64_t (&t)[K], uint64_t (&u)[K])
 template <int K, int G, typename KeyOf>
 __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (&t)[K])
 {
+    if constexpr (K >= 32) {
+        // at most K/2 elements per lane: sort those, the zero sentinels stay below
+        if (n <= G * (K / 2)) {
+            uint64_t c[K / 2];
+#pragma unroll
+            for (int q = 0; q < K / 2; ++q) {
+                const int i = q * G + g;
+                c[q] = i < n ? key_of(i) : 0;
+            }
+            chunk_sort<K / 2, true>(c);
+#pragma unroll
+            for (int q = 0; q < K; ++q) t[q] = q < K / 2 ? c[q] : 0;
+            group_merge<K, G>(t);
+            return;
+        }
+    }
     if (n <= 0) list_clear<K>(t);
     for (int base = 0; base < n; base += G * K) {
         uint64_t c[K];
@@ -253,49 +269,53 @@ __device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v
     }
 }
 
-// Output stage of one route row from its candidate list t (top-K, descending):
-// chosen slots in ascending order, softmax over their sums; lane g of the
-// group writes the outputs w with w % G == g.
+// Output stage of one route row from its candidate list t (top-K, descending;
+// every lane of the group holds it): the chosen slots in ascending order and a
+// softmax over their sums.  Lane g of the group handles the picks w with
+// w % G == g: a pick's output position is the number of chosen slots below its
+// own (slots are distinct), so no sort is needed.  The max runs over the picks
+// in list order; the exponentials are summed per lane, then across the group by
+// a fixed butterfly, so the result is deterministic.
 template <int K, int G>
 __device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, int tie, int g, bool live,
                                              int64_t *index_row, float *weight_row)
 {
-    uint64_t u[K];
-#pragma unroll
-    for (int w = 0; w < K; ++w) {
-        if (w < width) {
-            const uint32_t slot = rank_index(t[w], tie);
-            const float s = order_value((uint32_t)(t[w] >> 32));
-            u[w] = ((uint64_t)slot << 32) | __float_as_uint(s);
-        } else {
-            u[w] = ~0ull;
-        }
-    }
-    chunk_sort<K, false>(u);
+    uint32_t slot[K];
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < K; ++w) {
+        slot[w] = w < width ? rank_index(t[w], tie) : 0xFFFFFFFFu;
         if (w < width) {
-            const float s = __uint_as_float((uint32_t)u[w]);
+            const float s = order_value((uint32_t)(t[w] >> 32));
             m = (s > m || s != s) ? s : m;
         }
     }
-    float e[K];
-    float total = 0.0f;
+    constexpr int MINE = (K + G - 1) / G;
+    float e[MINE];
+    float part = 0.0f;
 #pragma unroll
-    for (int w = 0; w < K; ++w) {
-        if (w < width) {
-            e[w] = expf(__uint_as_float((uint32_t)u[w]) - m);
-            total += e[w];
+    for (int u = 0; u < MINE; ++u) {
+        const int w = u * G + g;
+        e[u] = 0.0f;
+        if (w < width && w < K) {
+            e[u] = expf(order_value((uint32_t)(t[w] >> 32)) - m);
+            part += e[u];
         }
     }
+    float total = part;
+#pragma unroll
+    for (int x = 1; x < G; x <<= 1) total += __shfl_xor(total, x);
     const float inv = 1.0f / total;
     if (live) {
 #pragma unroll
-        for (int w = 0; w < K; ++w) {
-            if (w < width && w % G == g) {
-                index_row[w] = (int64_t)(u[w] >> 32);
-                weight_row[w] = e[w] * inv;
+        for (int u = 0; u < MINE; ++u) {
+            const int w = u * G + g;
+            if (w < width && w < K) {
+                int rank = 0;
+#pragma unroll
+                for (int j = 0; j < K; ++j) rank += slot[j] < slot[w] ? 1 : 0;
+                index_row[rank] = (int64_t)slot[w];
+                weight_row[rank] = e[u] * inv;
             }
         }
     }
