@@ -324,6 +324,35 @@ struct ProposalTerms {
     }
 };
 
+// ReadGradTerms: the gathered rows' gradient in the read's backward,
+//     weights[e] * grad_out[e / width]
+// (the autograd of out = sum_j w_j row_j, S/memory/routing.py:27-28), added
+// onto a gradient bank in entry order: the result of the reference's
+// accumulating index backward of flat[address] (S/memory/routing.py:42).
+struct ReadGradTerms {
+    const float *weights, *grad_out;
+    int64_t D;
+    uint32_t width;
+    struct Entry {
+        const float *g;
+        float w;
+    };
+    __device__ __forceinline__ Entry entry(int64_t ent) const
+    {
+        const uint32_t r = (uint32_t)ent / width;
+        return {grad_out + (int64_t)r * D, weights[ent]};
+    }
+    template <int VEC>
+    __device__ __forceinline__ void get(const Entry &e, int v, const float (&)[VEC], float (&x)[VEC]) const
+    {
+#pragma clang fp contract(off)
+        float g[VEC];
+        VecLoad<float, VEC>::load(e.g + (int64_t)v * VEC, g);
+#pragma unroll
+        for (int y = 0; y < VEC; ++y) x[y] = g[y] * e.w;
+    }
+};
+
 // One wavefront per window of `win` (a power of two <= 64) consecutive sorted
 // positions; lane groups of `lpr` lanes (one bank row each) walk the address
 // runs that start in the window, continuing past its end when a run does.
@@ -623,4 +652,30 @@ extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t ro
                                               unique_out, st);
     return launch_segment_t<bf16_t, float>(bank, rows, D, keys, src, error, sorted, entries, ebits, unique_out,
                                            st);
+}
+
+extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t D, const int64_t *addresses,
+                                        int64_t entries, int32_t width, const float *weights,
+                                        const float *grad_out, void *workspace, size_t workspace_bytes,
+                                        void *stream)
+{
+    if (rows < 1 || D < 1 || entries < 0 || width < 1)
+        return fail(GLSDM_ERR_ARG, "read_backward_rows: bad shape rows=%lld D=%lld entries=%lld width=%d",
+                    (long long)rows, (long long)D, (long long)entries, (int)width);
+    if (entries % width != 0)
+        return fail(GLSDM_ERR_ARG, "read_backward_rows: %lld entries are not whole rows of width %d",
+                    (long long)entries, (int)width);
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("read_backward_rows", rows, D, entries);
+    if (rc) return rc;
+    if (!grad_bank || !addresses || !weights || !grad_out) return fail(GLSDM_ERR_ARG, "read_backward_rows: null pointer");
+    const hipStream_t st = as_stream(stream);
+    const uint64_t *sorted = nullptr;
+    int ebits = 0;
+    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "read_backward_rows", &sorted,
+                          &ebits, st)))
+        return rc;
+    const ReadGradTerms src{weights, grad_out, D, (uint32_t)width};
+    return launch_segment_t<float, float>(grad_bank, rows, D, nullptr, src, grad_out, sorted, entries, ebits,
+                                          nullptr, st);
 }

@@ -16,11 +16,16 @@ this module                reference entry point it stands in for
 ``proposal_error``         ``S/runtime/dense.py:12-13`` (decay and error terms)
 ``commit_proposals``       ``dense.py:11-14`` + ``global_layer.py:44`` + ``commit``
 ``require_cuda``           ``S/memory/backends/primitives.py:7-12``
+``route_backward``         ``S/memory/backends/token.py:69-82``
+``read_backward_*``        autograd of ``S/memory/routing.py:27-28,42``
 =========================  ===================================================
 
 All tensors are torch-allocated on the caller's current stream; the library
-never allocates device memory and never synchronises.  Forward only: inputs
-that require gradients are rejected (the backward pass is not built yet).
+never allocates device memory and never synchronises.  ``route``,
+``snapshot_read``, ``routed_snapshot_read`` and ``commit`` are differentiable
+(their backward runs ``glsdm_route_backward``, ``glsdm_read_backward_weights``,
+``glsdm_read_backward_rows`` and a row gather); the other entry points are
+forward-only and reject inputs that require gradients.
 """
 import torch
 
@@ -47,10 +52,7 @@ def _square_root(slots):
     return half
 
 
-def route(scores, count, tie="lowest"):
-    """Product-key route of fp32 scores ``[..., 2*half]`` -> (index int64, weights fp32) ``[..., count]``."""
-    _no_grad(scores)
-    scores = scores.float().contiguous() if scores.dtype != torch.float32 else scores
+def _route(scores, count, tie):
     device = require_cuda(scores)
     half = scores.shape[-1] // 2
     if scores.shape[-1] != 2 * half or not 1 <= count <= half * half:
@@ -63,9 +65,44 @@ def route(scores, count, tie="lowest"):
     return index, weights
 
 
-def snapshot_read(values, index, weights, out_dtype=torch.float32):
-    """Weighted gather ``sum_j w_j * values[b, h, index_j]`` -> ``[B, T, H, D]``."""
-    _no_grad(values, weights)
+def route_backward(index, weights, grad_weights, half):
+    """Factor-score gradient ``[..., 2*half]`` fp32 of a route (token.py:69-82)."""
+    device = require_cuda(index, weights, grad_weights)
+    width = index.shape[-1]
+    out = torch.empty((*index.shape[:-1], 2 * half), dtype=torch.float32, device=device)
+    N.call("glsdm_route_backward", N.ptr(index), N.ptr(weights), N.ptr(grad_weights), index.numel() // width,
+           half, width, N.ptr(out), N.stream(device))
+    return out
+
+
+class _Route(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, scores, count, tie):
+        index, weights = _route(scores, count, tie)
+        ctx.save_for_backward(index, weights)
+        ctx.half = scores.shape[-1] // 2
+        ctx.mark_non_differentiable(index)
+        return index, weights
+
+    @staticmethod
+    def backward(ctx, _, grad_weights):
+        index, weights = ctx.saved_tensors
+        if grad_weights is None:
+            return None, None, None
+        return route_backward(index, weights, grad_weights.float().contiguous(), ctx.half), None, None
+
+
+def route(scores, count, tie="lowest"):
+    """Product-key route of fp32 scores ``[..., 2*half]`` -> (index int64, weights fp32) ``[..., count]``.
+
+    Differentiable w.r.t. ``scores`` through the weights (token.py:85-114)."""
+    scores = scores.float().contiguous() if scores.dtype != torch.float32 else scores.contiguous()
+    if torch.is_grad_enabled() and scores.requires_grad:
+        return _Route.apply(scores, count, tie)
+    return _route(scores, count, tie)
+
+
+def _read(values, index, weights, out_dtype):
     device = require_cuda(values, index, weights)
     B, H, S, D = values.shape
     if index.ndim != 4 or index.shape[0] != B or index.shape[2] != H or weights.shape != index.shape:
@@ -79,18 +116,73 @@ def snapshot_read(values, index, weights, out_dtype=torch.float32):
     return out
 
 
-def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="highest",
-                         out_dtype=torch.float32):
-    """Route fp32 scores ``[B, T, H, 2*half]`` and read the bank ``[B, H, half**2, D]``.
+def read_backward_weights(values, index, grad_out):
+    """``grad_w[b,t,h,j] = <grad_out[b,t,h], values[b,h,index[b,t,h,j]]>`` (fp32)."""
+    device = require_cuda(values, index, grad_out)
+    B, H, S, D = values.shape
+    T, width = index.shape[1], index.shape[3]
+    out = torch.empty(index.shape, dtype=torch.float32, device=device)
+    N.call("glsdm_read_backward_weights", N.ptr(values), N.dtype_code(values), B, H, S, D, T, width,
+           N.ptr(index), N.ptr(grad_out), N.ptr(out), N.stream(device))
+    return out
 
-    Returns ``(readings [B,T,H,D], index int64 [B,T,H,width] ascending, weights fp32)``.
-    ``allow_large_route`` is accepted for signature compatibility; every factor
-    extent up to 65535 is supported.
-    """
-    del allow_large_route
-    _no_grad(values, scores)
-    scores = scores if scores.dtype == torch.float32 else scores.float()
-    scores = scores.contiguous()
+
+def read_backward_rows(grad_bank, addresses, weights, grad_out, workspace=None):
+    """In place: ``grad_bank.view(-1, D)[addresses[e]] += weights[e] * grad_out[e // width]``,
+    each row's terms summed in entry order (fp32 ``grad_bank``)."""
+    device = require_cuda(grad_bank, addresses, weights, grad_out)
+    if grad_bank.dtype != torch.float32:
+        raise ValueError("read_backward_rows accumulates into an fp32 gradient")
+    D = grad_bank.shape[-1]
+    E, R = addresses.numel(), grad_out.numel() // D
+    if E == 0:
+        return grad_bank
+    if grad_out.shape[-1] != D or R == 0 or E % R != 0 or weights.numel() != E:
+        raise ValueError("read_backward_rows needs weights [E], grad_out [R, D] with E a multiple of R")
+    width = E // R
+    rows = grad_bank.numel() // D
+    need = commit_workspace_bytes(E, rows)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    N.call("glsdm_read_backward_rows", N.ptr(grad_bank), rows, D, N.ptr(addresses), E, width, N.ptr(weights),
+           N.ptr(grad_out), N.ptr(workspace), workspace.numel(), N.stream(device))
+    return grad_bank
+
+
+def _read_grads(ctx_values, index, weights, grad_out, need_values, need_weights):
+    grad_out = grad_out.float().contiguous()
+    grad_w = read_backward_weights(ctx_values, index, grad_out) if need_weights else None
+    grad_v = None
+    if need_values:
+        grad_v = torch.zeros(ctx_values.shape, dtype=torch.float32, device=ctx_values.device)
+        read_backward_rows(grad_v, absolute_addresses(ctx_values, index), weights, grad_out)
+        grad_v = grad_v.to(ctx_values.dtype)
+    return grad_v, grad_w
+
+
+class _SnapshotRead(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, values, index, weights, out_dtype):
+        ctx.save_for_backward(values, index, weights)
+        return _read(values, index, weights, out_dtype)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        values, index, weights = ctx.saved_tensors
+        grad_v, grad_w = _read_grads(values, index, weights, grad_out, ctx.needs_input_grad[0],
+                                     ctx.needs_input_grad[2])
+        return grad_v, None, grad_w, None
+
+
+def snapshot_read(values, index, weights, out_dtype=torch.float32):
+    """Weighted gather ``sum_j w_j * values[b, h, index_j]`` -> ``[B, T, H, D]``;
+    differentiable w.r.t. ``values`` and ``weights``."""
+    if torch.is_grad_enabled() and (values.requires_grad or weights.requires_grad):
+        return _SnapshotRead.apply(values, index, weights, out_dtype)
+    return _read(values, index, weights, out_dtype)
+
+
+def _routed_read(values, scores, width, tie, out_dtype):
     device = require_cuda(values, scores)
     B, H, S, D = values.shape
     if scores.ndim != 4 or scores.shape[0] != B or scores.shape[2] != H:
@@ -105,6 +197,48 @@ def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="hi
     N.call("glsdm_route_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, N.ptr(scores), width,
            N.TIES[tie], N.ptr(out), N.dtype_code(out), N.ptr(index), N.ptr(weights), N.stream(device))
     return out, index, weights
+
+
+class _RoutedRead(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, values, scores, width, tie, out_dtype):
+        out, index, weights = _routed_read(values, scores, width, tie, out_dtype)
+        ctx.save_for_backward(values, index, weights)
+        ctx.half = scores.shape[-1] // 2
+        ctx.mark_non_differentiable(index)
+        return out, index, weights
+
+    @staticmethod
+    def backward(ctx, grad_out, _, grad_weights):
+        values, index, weights = ctx.saved_tensors
+        need_v, need_s = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        grad_v, grad_w = None, None
+        if grad_out is not None:
+            grad_v, grad_w = _read_grads(values, index, weights, grad_out, need_v, need_s)
+        grad_s = None
+        if need_s:
+            total = grad_w if grad_weights is None else (
+                grad_weights.float() if grad_w is None else grad_w + grad_weights.float())
+            if total is not None:
+                grad_s = route_backward(index, weights, total.contiguous(), ctx.half)
+        return grad_v, grad_s, None, None, None
+
+
+def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="highest",
+                         out_dtype=torch.float32):
+    """Route fp32 scores ``[B, T, H, 2*half]`` and read the bank ``[B, H, half**2, D]``.
+
+    Returns ``(readings [B,T,H,D], index int64 [B,T,H,width] ascending, weights fp32)``;
+    differentiable w.r.t. ``values`` and ``scores`` (through readings and weights).
+    ``allow_large_route`` is accepted for signature compatibility; every factor
+    extent up to 65535 is supported.
+    """
+    del allow_large_route
+    scores = scores if scores.dtype == torch.float32 else scores.float()
+    scores = scores.contiguous()
+    if torch.is_grad_enabled() and (values.requires_grad or scores.requires_grad):
+        return _RoutedRead.apply(values, scores, width, tie, out_dtype)
+    return _routed_read(values, scores, width, tie, out_dtype)
 
 
 def score(queries, subkeys):
@@ -214,20 +348,7 @@ def commit_workspace_bytes(entries, rows):
     return size.value
 
 
-def commit(memory, indices, deltas, keys=None, donate=False, workspace=None, unique=None):
-    """Deterministic commit of ``deltas [E, D]`` at absolute rows ``indices [E]``.
-
-    ``memory`` is any contiguous tensor whose last dimension is D (e.g. the
-    ``[B, H, S, D]`` bank).  Returns the updated bank: a new tensor, or
-    ``memory`` itself updated in place when ``donate=True`` (the caller gives
-    up the old contents; no full-bank copy is made).
-
-    ``keys`` (int64 [E], default: arrival order) orders colliding deltas: each
-    address's deltas are summed from +0 in ascending (key, entry) order.
-    ``workspace`` (uint8 device tensor) and ``unique`` (int64 [1] device
-    counter, incremented by the number of touched rows) are optional.
-    """
-    _no_grad(memory, deltas)
+def _commit(memory, indices, deltas, keys, donate, workspace, unique):
     device = require_cuda(memory, indices, deltas, keys)
     if indices.dtype != torch.int64 or (keys is not None and keys.dtype != torch.int64):
         raise ValueError("commit needs int64 addresses and keys")
@@ -247,6 +368,47 @@ def commit(memory, indices, deltas, keys=None, donate=False, workspace=None, uni
            N.dtype_code(deltas), N.ptr(keys), E, N.ptr(workspace), workspace.numel(), N.ptr(unique),
            N.stream(device))
     return out
+
+
+class _Commit(torch.autograd.Function):
+    """backends/commit.py:36-54: the bank's gradient passes through; each delta's
+    gradient is the bank gradient's row at its address (0 for dropped entries)."""
+
+    @staticmethod
+    def forward(ctx, memory, indices, deltas, keys):
+        ctx.save_for_backward(indices)
+        ctx.delta_shape, ctx.delta_dtype = deltas.shape, deltas.dtype
+        return _commit(memory, indices, deltas, keys, False, None, None)
+
+    @staticmethod
+    def backward(ctx, incoming):
+        (indices,) = ctx.saved_tensors
+        incoming = incoming.contiguous()
+        grad_d = None
+        if ctx.needs_input_grad[2]:
+            grad_d = gather_flat(incoming.float(), indices.reshape(-1)).reshape(ctx.delta_shape).to(ctx.delta_dtype)
+        return incoming, None, grad_d, None
+
+
+def commit(memory, indices, deltas, keys=None, donate=False, workspace=None, unique=None):
+    """Deterministic commit of ``deltas [E, D]`` at absolute rows ``indices [E]``.
+
+    ``memory`` is any contiguous tensor whose last dimension is D (e.g. the
+    ``[B, H, S, D]`` bank).  Returns the updated bank: a new tensor, or
+    ``memory`` itself updated in place when ``donate=True`` (the caller gives
+    up the old contents; no full-bank copy is made).
+
+    ``keys`` (int64 [E], default: arrival order) orders colliding deltas: each
+    address's deltas are summed from +0 in ascending (key, entry) order.
+    ``workspace`` (uint8 device tensor) and ``unique`` (int64 [1] device
+    counter, incremented by the number of touched rows) are optional.
+    Differentiable w.r.t. ``memory`` and ``deltas`` (not with ``donate=True``).
+    """
+    if torch.is_grad_enabled() and (memory.requires_grad or deltas.requires_grad):
+        if donate:
+            raise ValueError("commit: donate=True cannot be differentiated (the input bank is overwritten)")
+        return _Commit.apply(memory, indices, deltas, keys)
+    return _commit(memory, indices, deltas, keys, donate, workspace, unique)
 
 
 def _proposal_rows(prediction, target, beta, log_decay):

@@ -243,6 +243,47 @@ int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t rows, int64_t
                            const float *mass, int64_t heads, void *workspace, size_t workspace_bytes,
                            int64_t *unique_out, void *stream);
 
+/*
+ * Backward of the route: the factor-score gradient of a route's weights.
+ *   index [rows, width] int64 (slots), weights [rows, width] fp32 (the route's
+ *   softmax), grad_weights [rows, width] fp32 in; grad_scores [rows, 2*half]
+ *   fp32 out: with g_j = w_j * (gw_j - sum_v w_v gw_v), column c < half is the
+ *   sum of g_j over the picks with slot / half == c, column half + c the sum
+ *   over the picks with slot % half == c (in pick order), 0 elsewhere.
+ * Replaces: S/memory/backends/token.py:69-82 (_route_backward) and the autograd
+ * of S/memory/routing.py:10-26 (torch_routed_read's route).
+ */
+int glsdm_route_backward(const int64_t *index, const float *weights, const float *grad_weights,
+                         int64_t rows, int32_t half, int32_t width, float *grad_scores, void *stream);
+
+/*
+ * Backward of the snapshot read w.r.t. its weights:
+ *   grad_weights[b,t,h,j] = sum_d grad_out[b,t,h,d] * bank[b,h,index[b,t,h,j],d]
+ * (fp32; bank [B,H,S,D] of bank_dtype; out-of-range slots give 0).
+ * Replaces: the weights' gradient in the autograd of S/memory/routing.py:27-28
+ * ((rows * weights).sum(-2)) and URM's read backward (S/memory/backends/urm.py).
+ */
+int glsdm_read_backward_weights(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S,
+                                int64_t D, int64_t T, int32_t width, const int64_t *index,
+                                const float *grad_out, float *grad_weights, void *stream);
+
+/*
+ * Backward of the snapshot read w.r.t. the bank rows, accumulated in place:
+ *   grad_bank[addresses[e]] += weights[e] * grad_out[e / width]
+ * for every in-range entry, each address's terms summed from +0 in entry order
+ * and then added once (no float atomics; deterministic).  grad_bank [rows, D]
+ * fp32; addresses [entries] int64 absolute rows of grad_bank (e.g. those of
+ * glsdm_absolute_addresses, or h*S + slot to fold the requests' replicas into
+ * one [H,S,D] gradient); weights [entries]; grad_out [entries / width, D].
+ * Workspace: glsdm_commit_workspace_bytes(entries, rows).
+ * Replaces: the accumulating index backward of S/memory/routing.py:42
+ * (flat[address]) in the autograd of the read, without the dense full-bank
+ * gradient the reference's read backward materialises per call.
+ */
+int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t D, const int64_t *addresses,
+                             int64_t entries, int32_t width, const float *weights, const float *grad_out,
+                             void *workspace, size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

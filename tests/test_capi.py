@@ -13,7 +13,8 @@ def test_header_declares_the_expected_surface():
     for required in ("glsdm_route", "glsdm_read", "glsdm_route_read", "glsdm_score", "glsdm_commit",
                      "glsdm_commit_workspace_bytes", "glsdm_absolute_addresses", "glsdm_proposal_keys",
                      "glsdm_gather_rows", "glsdm_version", "glsdm_last_error", "glsdm_proposal_error",
-                     "glsdm_proposal_delta", "glsdm_commit_proposals"):
+                     "glsdm_proposal_delta", "glsdm_commit_proposals", "glsdm_route_backward",
+                     "glsdm_read_backward_weights", "glsdm_read_backward_rows"):
         assert required in names
 
 
@@ -75,6 +76,17 @@ def test_proposal_envelopes():
                None, None) == N.ERR_ARG
     assert _rc("glsdm_commit_proposals", None, 0, 16, 4, None, None, 0, 4, None, None, None, None, 1, None, 0,
                None, None) == N.OK
+
+
+def test_backward_envelopes():
+    one = ctypes.c_void_p(16)
+    assert _rc("glsdm_route_backward", one, one, one, 4, 8, 65, one, None) == N.ERR_UNSUPPORTED   # width
+    assert _rc("glsdm_route_backward", one, one, None, 4, 8, 4, one, None) == N.ERR_ARG           # null
+    assert _rc("glsdm_route_backward", None, None, None, 0, 8, 4, None, None) == N.OK            # empty
+    assert _rc("glsdm_read_backward_weights", one, 0, 1, 1, 16, 4096, 2, 4, one, one, one, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_read_backward_weights", one, 5, 1, 1, 16, 64, 2, 4, one, one, one, None) == N.ERR_ARG
+    assert _rc("glsdm_read_backward_rows", one, 16, 4, one, 10, 4, one, one, None, 0, None) == N.ERR_ARG  # 10 % 4
+    assert _rc("glsdm_read_backward_rows", one, 16, 4, one, 8, 4, one, one, None, 0, None) == N.ERR_WORKSPACE
 
 
 def test_read_and_score_envelopes():

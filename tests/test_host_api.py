@@ -65,8 +65,14 @@ def test_backend_and_device_checks():
 
 
 def test_forward_only_guard():
-    s = torch.zeros(2, 8, requires_grad=True)
+    # scoring, proposals and the fused commit are forward-only
+    q = torch.zeros(1, 2, 1, 32, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.zeros(1, 64, 32, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError):
+        hip.score(q, k)
+    # the differentiable route still never falls back to the CPU
+    s = torch.zeros(2, 8, requires_grad=True)
+    with pytest.raises(ValueError, match="CUDA"):
         hip.route(s, 2)
 
 
