@@ -125,9 +125,9 @@ class Pipeline:
       durations stop being a clean roofline measurement), so it is not the default.
     """
 
-    def __init__(self, cfg, device, write_path="deltas"):
+    def __init__(self, cfg, device, write_path="deltas", backward=False):
         from glsdm import _native as N
-        self.N, self.cfg, self.dev, self.write_path = N, cfg, device, write_path
+        self.N, self.cfg, self.dev, self.write_path, self.backward = N, cfg, device, write_path, backward
         keys, bank, qr, qw, delta = make_inputs(cfg)
         B, T, C, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "C", "H", "half", "dk", "D", "k"))
         self.epochs = T // C
@@ -160,6 +160,17 @@ class Pipeline:
             if write_path == "proposals-materialised":
                 self.rows_buf = torch.empty(B, C, H, k, D, dtype=self.bank.dtype, device=device)
                 self.dbuf = torch.empty(B, C, H, k, D, dtype=torch.float32, device=device)
+        if backward:
+            # read backward into the learned [H, S, D] bank's fp32 gradient: the
+            # requests' replicas fold onto one row (address h*S + slot)
+            g = torch.Generator("cpu").manual_seed(2)
+            self.grad_out = (torch.randn(B, C, H, D, generator=g) * 0.01).to(device)
+            self.grad_w = torch.empty(B, C, H, k, dtype=torch.float32, device=device)
+            self.grad_scores = torch.empty(B, C, H, 2 * half, dtype=torch.float32, device=device)
+            self.grad_bank = torch.zeros(H * half * half, D, dtype=torch.float32, device=device)
+            self.fold = [torch.empty(B, C, H, k, dtype=torch.int64, device=device) for _ in range(self.epochs)]
+            N.call("glsdm_commit_workspace_bytes", self.E, H * half * half, ctypes.byref(size))
+            self.bw_ws = torch.empty(size.value, dtype=torch.uint8, device=device)
         self.mem_stream = torch.cuda.current_stream(device)
         self.route_stream = torch.cuda.Stream(device)          # default priority
         self.routed = [torch.cuda.Event() for _ in range(self.epochs)]
@@ -199,6 +210,20 @@ class Pipeline:
         self._timed("read", stream, lambda: N.call(
             "glsdm_read", p(self.bank), dt, B, H, half * half, D, C, k, p(self.idx[e]), p(self.w[e]),
             p(self.out), N.F32, st))
+        if self.backward:
+            S = half * half
+            self._timed("read_bw_weights", stream, lambda: N.call(
+                "glsdm_read_backward_weights", p(self.bank), dt, B, H, S, D, C, k, p(self.idx[e]),
+                p(self.grad_out), p(self.grad_w), st))
+            self._timed("route_bw", stream, lambda: N.call(
+                "glsdm_route_backward", p(self.idx[e]), p(self.w[e]), p(self.grad_w), B * C * H, half, k,
+                p(self.grad_scores), st))
+            # [B, C, H, k] seen as one request of B*C tokens: addresses h*S + slot
+            self._timed("fold", stream, lambda: N.call(
+                "glsdm_absolute_addresses", p(self.idx[e]), 1, B * C, H, k, S, p(self.fold[e]), st))
+            self._timed("read_bw_rows", stream, lambda: N.call(
+                "glsdm_read_backward_rows", p(self.grad_bank), H * S, D, p(self.fold[e]), self.E, k,
+                p(self.w[e]), p(self.grad_out), p(self.bw_ws), self.bw_ws.numel(), st))
         if self.write_path == "deltas":
             self._timed("commit", stream, lambda: N.call(
                 "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.delta[e]), dt,
@@ -332,6 +357,10 @@ def main():
     ap.add_argument("--compare-schedules", action="store_true",
                     help="also time the other schedule (reported as ms_per_step_other_schedule)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--backward", action="store_true",
+                    help="also run the read's backward every epoch: weights' and factor scores' gradients, and "
+                         "the bank rows' gradient folded into the learned [H, S, D] bank (reported alongside; "
+                         "not the BASELINE protocol)")
     ap.add_argument("--write-path", choices=("deltas", "proposals", "proposals-materialised"), default="deltas",
                     help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
                          "path with the fused proposal commit; proposals-materialised: the same work with "
@@ -349,7 +378,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
-    pipe = Pipeline(cfg, dev, args.write_path)
+    pipe = Pipeline(cfg, dev, args.write_path, args.backward)
     unique = pipe.unique_rows()
     for _ in range(args.warmup):
         pipe.step()
@@ -454,10 +483,11 @@ def main():
                                f"({epochs} epochs of {cfg['C']}) H={cfg['H']} M={cfg['half'] ** 2} dk={cfg['dk']} "
                                f"D={cfg['D']} k={cfg['k']} {'bf16' if cfg['dtype'] == torch.bfloat16 else 'fp32'}"
                                f"{' Zipf-skewed' if cfg['skew'] else ''}, fused score-route + read + fused "
-                               "score-route + keys + " + WRITE_PATHS[args.write_path],
+                               "score-route + keys + " + WRITE_PATHS[args.write_path]
+                               + (" + read backward (route, weights, bank rows)" if args.backward else ""),
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
                    "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
-                   "write_path": args.write_path, "parallelism": "single GPU"},
+                   "write_path": args.write_path, "backward": args.backward, "parallelism": "single GPU"},
         "roofline": roof,
         "read_commit_hbm": {"bytes_per_step": alg_total, "seconds_per_step": rc_time,
                             "achieved_GBps": round(alg_total / rc_time / 1e9, 1),

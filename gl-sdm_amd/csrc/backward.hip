@@ -27,6 +27,7 @@ __device__ __forceinline__ float wave_sum(float x)
 }
 
 // One wavefront per route row.
+template <bool QUAD>
 __global__ __launch_bounds__(256) void route_backward_kernel(const int64_t *__restrict__ index,
                                                              const float *__restrict__ weights,
                                                              const float *__restrict__ grad_weights, int64_t rows,
@@ -59,43 +60,65 @@ __global__ __launch_bounds__(256) void route_backward_kernel(const int64_t *__re
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // column c of factor f gets the picks whose sub-key of factor f is c, in pick order
     float *out = grad_scores + r * 2 * (int64_t)half;
-    for (int c = lane; c < 2 * half; c += 64) {
-        const int f = c >= half ? 1 : 0, sub = f ? c - half : c;
-        float acc = 0.0f;
-        for (int j = 0; j < width; ++j)
-            if (s_sub[wave][f][j] == sub) acc += s_g[wave][j];
-        out[c] = acc;
+    if (QUAD) {
+        // four adjacent columns per lane (one factor: half % 4 == 0), one 16-byte store
+        for (int c = 4 * lane; c < 2 * half; c += 256) {
+            const int f = c >= half ? 1 : 0, sub = f ? c - half : c;
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int j = 0; j < width; ++j) {
+                const int d = s_sub[wave][f][j] - sub;
+                const float gj = s_g[wave][j];
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    if (d == x) acc[x] += gj;
+            }
+            *reinterpret_cast<float4 *>(out + c) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+        }
+    } else {
+        for (int c = lane; c < 2 * half; c += 64) {
+            const int f = c >= half ? 1 : 0, sub = f ? c - half : c;
+            float acc = 0.0f;
+            for (int j = 0; j < width; ++j)
+                if (s_sub[wave][f][j] == sub) acc += s_g[wave][j];
+            out[c] = acc;
+        }
     }
 }
 
 // One wavefront per read row: grad_w[r, j] = <grad_out[r], bank[addr(r, j)]>.
+// Lane groups of `lpr` lanes (16-byte row pieces) take picks j = grp, grp + ng,
+// ...; each group reduces its dot product over its own lanes.
 template <typename TB, int VEC, int CH>
 __global__ __launch_bounds__(256) void read_backward_weights_kernel(const TB *__restrict__ bank, int64_t H,
                                                                     int64_t S, int64_t D, int64_t T, int width,
                                                                     const int64_t *__restrict__ index,
                                                                     const float *__restrict__ grad_out,
                                                                     float *__restrict__ grad_weights, int64_t rows,
-                                                                    int nv)
+                                                                    int nv, int lpr)
 {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);   // (b*T + t)*H + h
     if (r >= rows) return;   // wave-uniform
+    const int ng = 64 / lpr, grp = lane / lpr, li = lane % lpr;
     const int64_t h = r % H, b = r / H / T;
     float go[CH][VEC];
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-        const int v = lane + c * 64;
+        const int v = li + c * lpr;
         if (v < nv) VecLoad<float, VEC>::load(grad_out + r * D + (int64_t)v * VEC, go[c]);
     }
     const TB *part = bank + (b * H + h) * S * D;
-    for (int j = 0; j < width; ++j) {
-        const int64_t slot = index[r * width + j];
+    // every group runs the same number of rounds, so the shuffles see whole groups
+    const int rounds = (width + ng - 1) / ng;
+    for (int q = 0; q < rounds; ++q) {
+        const int j = q * ng + grp;
+        const int64_t slot = j < width ? index[r * width + j] : -1;
         float acc = 0.0f;
         if (slot >= 0 && slot < S) {
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-                const int v = lane + c * 64;
+                const int v = li + c * lpr;
                 if (v < nv) {
                     float x[VEC];
                     VecLoad<TB, VEC>::load(part + slot * D + (int64_t)v * VEC, x);
@@ -107,24 +130,25 @@ __global__ __launch_bounds__(256) void read_backward_weights_kernel(const TB *__
                 }
             }
         }
-        const float total = wave_sum(acc);
-        if (lane == 0) grad_weights[r * width + j] = total;
+        for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        if (li == 0 && j < width) grad_weights[r * width + j] = acc;
     }
 }
 
 template <typename TB, int VEC>
 static void launch_rbw(const void *bank, int64_t H, int64_t S, int64_t D, int64_t T, int width,
-                       const int64_t *index, const float *grad_out, float *grad_weights, int64_t rows, int nv,
-                       int ch, hipStream_t st)
+                       const int64_t *index, const float *grad_out, float *grad_weights, int64_t rows,
+                       const RowPlan &p, hipStream_t st)
 {
     const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
     const TB *bk = static_cast<const TB *>(bank);
 #define GLSDM_RBW(C)                                                                                        \
     hipLaunchKernelGGL((read_backward_weights_kernel<TB, VEC, C>), grid, block, 0, st, bk, H, S, D, T, width, \
-                       index, grad_out, grad_weights, rows, nv)
-    switch (ch) {
+                       index, grad_out, grad_weights, rows, p.nv, p.lpr)
+    switch (p.ch) {
     case 1: GLSDM_RBW(1); break;
     case 2: GLSDM_RBW(2); break;
+    case 3:
     case 4: GLSDM_RBW(4); break;
     default: GLSDM_RBW(8); break;
     }
@@ -144,8 +168,13 @@ extern "C" int glsdm_route_backward(const int64_t *index, const float *weights, 
     if (rows == 0) return GLSDM_OK;
     if (!index || !weights || !grad_weights || !grad_scores) return fail(GLSDM_ERR_ARG, "route_backward: null pointer");
     if (ceil_div(rows, 4) > (int64_t)UINT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "route_backward: too many rows");
-    hipLaunchKernelGGL(route_backward_kernel, dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0, as_stream(stream),
-                       index, weights, grad_weights, rows, half, width, grad_scores);
+    const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
+    if (half % 4 == 0 && (reinterpret_cast<uintptr_t>(grad_scores) & 15) == 0)
+        hipLaunchKernelGGL(route_backward_kernel<true>, grid, block, 0, as_stream(stream), index, weights,
+                           grad_weights, rows, half, width, grad_scores);
+    else
+        hipLaunchKernelGGL(route_backward_kernel<false>, grid, block, 0, as_stream(stream), index, weights,
+                           grad_weights, rows, half, width, grad_scores);
     return check_launch("route_backward_kernel");
 }
 
@@ -163,17 +192,18 @@ extern "C" int glsdm_read_backward_weights(const void *bank, int32_t bank_dtype,
     if (!bank || !index || !grad_out || !grad_weights) return fail(GLSDM_ERR_ARG, "read_backward_weights: null pointer");
     if (ceil_div(rows, 4) > (int64_t)UINT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "read_backward_weights: too many rows");
     const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(grad_out)) & 15) == 0;
-    const int vec = (D % 4 == 0 && aligned) ? 4 : 1;
-    const int nv = (int)(D / vec);
-    int ch = (int)ceil_div(nv, 64);
-    if (ch > 2) ch = ch <= 4 ? 4 : 8;
     const hipStream_t st = as_stream(stream);
+    // 16-byte pieces of the bank row (8 bf16 or 4 fp32 per lane), else scalar
+    const RowPlan p = row_plan(D, dtype_size(bank_dtype));
+    const bool vector = p.vec > 1 && aligned;
+    if (!vector && D > 512)
+        return fail(GLSDM_ERR_UNSUPPORTED, "read_backward_weights: D=%lld needs 16-byte rows above 512", (long long)D);
     if (bank_dtype == GLSDM_F32) {
-        if (vec == 4) launch_rbw<float, 4>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, nv, ch, st);
-        else launch_rbw<float, 1>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, nv, ch, st);
+        if (vector) launch_rbw<float, 4>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, p, st);
+        else launch_rbw<float, 1>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, row_plan(D, 16), st);
     } else {
-        if (vec == 4) launch_rbw<bf16_t, 4>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, nv, ch, st);
-        else launch_rbw<bf16_t, 1>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, nv, ch, st);
+        if (vector) launch_rbw<bf16_t, 8>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, p, st);
+        else launch_rbw<bf16_t, 1>(bank, H, S, D, T, width, index, grad_out, grad_weights, rows, row_plan(D, 16), st);
     }
     return check_launch("read_backward_weights_kernel");
 }
