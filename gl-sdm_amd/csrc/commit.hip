@@ -48,7 +48,7 @@ constexpr int SORT_THREADS = GLSDM_SORT_THREADS;       // >= RADIX: threads belo
 #define GLSDM_SORT_ITEMS 8
 #endif
 #ifndef GLSDM_PACK_BLOCKS
-#define GLSDM_PACK_BLOCKS 128
+#define GLSDM_PACK_BLOCKS 256
 #endif
 constexpr int SORT_ITEMS = GLSDM_SORT_ITEMS;            // per thread
 constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // entries per tile
@@ -353,11 +353,59 @@ struct ReadGradTerms {
     }
 };
 
+// Where the segment kernel reads each touched row's old value and writes its
+// new one.
+//
+// DenseRows: the bank [rows, D] itself, in place.
+template <typename TB> struct DenseRows {
+    TB *bank;
+    int64_t D;
+    __device__ __forceinline__ const TB *old_row(int64_t a) const { return bank + a * D; }
+    __device__ __forceinline__ TB *new_row(int64_t a, int, int) const { return bank + a * D; }
+};
+
+// OverlayRows: a shared base [H*S, D] and, per request, a slot map [B*H*S]
+// (-1: the base row) into a pool of rows [capacity, D].  Address
+// a = (b*H + h)*S + slot reads pool row map[a] or base row a % (H*S); its new
+// value goes to its pool row, allocated on first write by one atomic per
+// touched row (pool positions are arbitrary, the values are not).  A full pool
+// drops the row's update and sets *overflow.
+template <typename TB> struct OverlayRows {
+    const TB *base;
+    int32_t *map;
+    TB *pool;
+    int64_t D, hs, capacity;
+    uint32_t *count, *overflow;
+    __device__ __forceinline__ const TB *old_row(int64_t a) const
+    {
+        const int32_t m = map[a];
+        return m >= 0 ? pool + (int64_t)m * D : base + (a % hs) * D;
+    }
+    // every lane of the run's group calls it; `li` is the lane within the group,
+    // `first` the group's first lane
+    __device__ __forceinline__ TB *new_row(int64_t a, int li, int first) const
+    {
+        int32_t m = map[a];
+        if (m < 0) {
+            uint32_t r = 0;
+            if (li == 0) r = atomicAdd(count, 1u);
+            r = (uint32_t)__shfl((int)r, first);
+            if ((int64_t)r >= capacity) {
+                if (li == 0) atomicOr(overflow, 1u);
+                return nullptr;
+            }
+            if (li == 0) map[a] = (int32_t)r;
+            m = (int32_t)r;
+        }
+        return pool + (int64_t)m * D;
+    }
+};
+
 // One wavefront per window of `win` (a power of two <= 64) consecutive sorted
 // positions; lane groups of `lpr` lanes (one bank row each) walk the address
 // runs that start in the window, continuing past its end when a run does.
-template <typename TB, typename SRC, int VEC, int CH>
-__global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int64_t rows, int64_t D,
+template <typename TB, typename SRC, typename ROWS, int VEC, int CH>
+__global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t rows, int64_t D,
                                                       const int64_t *__restrict__ keys, const SRC src,
                                                       const uint64_t *__restrict__ sorted, int64_t n, int ebits,
                                                       int nv, int lpr, int win,
@@ -410,7 +458,7 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
         // run length: positions after the head with the same address
         int len = 1;
         while (p0 + h + len < n && (int64_t)(word_at(h + len) >> ebits) == row_addr) ++len;
-        TB *row = bank + row_addr * D;
+        const TB *row = store.old_row(row_addr);
         float old[CH][VEC], acc[CH][VEC];
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
@@ -459,20 +507,22 @@ __global__ __launch_bounds__(256) void segment_kernel(TB *__restrict__ bank, int
                 last_e = best_e;
             }
         }
+        TB *dst = store.new_row(row_addr, li, lane - li);
+        if (!dst) continue;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
             if (v < nv) {
 #pragma unroll
                 for (int x = 0; x < VEC; ++x) old[c][x] = old[c][x] + acc[c][x];
-                VecStore<TB, VEC>::store(row + (int64_t)v * VEC, old[c]);
+                VecStore<TB, VEC>::store(dst + (int64_t)v * VEC, old[c]);
             }
         }
     }
 }
 
-template <typename TB, int VEC, typename SRC>
-static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
+template <typename TB, int VEC, typename SRC, typename ROWS>
+static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                              const uint64_t *sorted, int64_t n, int ebits, const RowPlan &p,
                              int64_t *unique_out, hipStream_t st)
 {
@@ -483,11 +533,10 @@ static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t 
     int win = 64;
     while (win > groups && ceil_div(n, win) < GLSDM_SEG_WAVES) win >>= 1;
     const dim3 grid((unsigned)ceil_div(n, 4 * win)), block(256);
-    TB *bk = static_cast<TB *>(bank);
     auto *u = reinterpret_cast<unsigned long long *>(unique_out);
-#define GLSDM_SEG_LAUNCH(C)                                                                                    \
-    hipLaunchKernelGGL((segment_kernel<TB, SRC, VEC, C>), grid, block, 0, st, bk, rows, D, keys, src, sorted, n, \
-                       ebits, p.nv, p.lpr, win, u)
+#define GLSDM_SEG_LAUNCH(C)                                                                                 \
+    hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C>), grid, block, 0, st, store, rows, D, keys, src, \
+                       sorted, n, ebits, p.nv, p.lpr, win, u)
     switch (p.ch) {
     case 1: GLSDM_SEG_LAUNCH(1); break;
     case 2: GLSDM_SEG_LAUNCH(2); break;
@@ -501,21 +550,31 @@ static int launch_segment_ch(void *bank, int64_t rows, int64_t D, const int64_t 
 
 // One vector width for bank and delta rows: the wider element type's 16-byte
 // vector when D and the row pointers allow it, else scalar accesses.
+template <typename TB, typename TD, typename SRC, typename ROWS>
+static int launch_segment_rows(const ROWS &store, uintptr_t row_bits, int64_t rows, int64_t D, const int64_t *keys,
+                               const SRC &src, const void *delta_rows, const uint64_t *sorted, int64_t n,
+                               int ebits, int64_t *unique_out, hipStream_t st)
+{
+    constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
+    const bool aligned = ((row_bits | reinterpret_cast<uintptr_t>(delta_rows)) & 15) == 0;
+    if (D % VEC == 0 && aligned) {
+        RowPlan p{VEC, (int)(D / VEC), 0, 0};
+        p.lpr = pow2_ceil(p.nv) < 64 ? pow2_ceil(p.nv) : 64;
+        p.ch = (int)ceil_div(p.nv, p.lpr);
+        return launch_segment_ch<TB, VEC>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
+    }
+    RowPlan p{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
+    return launch_segment_ch<TB, 1>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
+}
+
+// The bank itself as the row store.
 template <typename TB, typename TD, typename SRC>
 static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                             const void *delta_rows, const uint64_t *sorted, int64_t n, int ebits,
                             int64_t *unique_out, hipStream_t st)
 {
-    constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
-    const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(delta_rows)) & 15) == 0;
-    if (D % VEC == 0 && aligned) {
-        RowPlan p{VEC, (int)(D / VEC), 0, 0};
-        p.lpr = pow2_ceil(p.nv) < 64 ? pow2_ceil(p.nv) : 64;
-        p.ch = (int)ceil_div(p.nv, p.lpr);
-        return launch_segment_ch<TB, VEC>(bank, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
-    }
-    RowPlan p{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
-    return launch_segment_ch<TB, 1>(bank, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
+    return launch_segment_rows<TB, TD>(DenseRows<TB>{static_cast<TB *>(bank), D}, reinterpret_cast<uintptr_t>(bank),
+                                       rows, D, keys, src, delta_rows, sorted, n, ebits, unique_out, st);
 }
 
 }  // namespace glsdm
@@ -678,4 +737,42 @@ extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t 
     const ReadGradTerms src{weights, grad_out, D, (uint32_t)width};
     return launch_segment_t<float, float>(grad_bank, rows, D, nullptr, src, grad_out, sorted, entries, ebits,
                                           nullptr, st);
+}
+
+extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                                    int32_t *map, void *pool, int64_t capacity, uint32_t *counters,
+                                    const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                                    const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
+                                    int64_t *unique_out, void *stream)
+{
+    if (B < 1 || H < 1 || S < 1 || D < 1 || entries < 0 || capacity < 0)
+        return fail(GLSDM_ERR_ARG, "overlay_commit: bad shape");
+    if (!dtype_ok(dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "overlay_commit: bad dtype");
+    if (capacity > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "overlay_commit: capacity above 2^31-1 rows");
+    if (entries == 0) return GLSDM_OK;
+    const int64_t rows = B * H * S;
+    int rc = check_commit("overlay_commit", rows, D, entries);
+    if (rc) return rc;
+    if (!base || !map || !pool || !counters || !addresses || !deltas)
+        return fail(GLSDM_ERR_ARG, "overlay_commit: null pointer");
+    const hipStream_t st = as_stream(stream);
+    const uint64_t *sorted = nullptr;
+    int ebits = 0;
+    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "overlay_commit", &sorted, &ebits,
+                          st)))
+        return rc;
+    const uintptr_t row_bits = reinterpret_cast<uintptr_t>(base) | reinterpret_cast<uintptr_t>(pool);
+#define GLSDM_OVERLAY(TB, TD)                                                                                  \
+    {                                                                                                         \
+        const OverlayRows<TB> ov{static_cast<const TB *>(base), map, static_cast<TB *>(pool), D, H * S,       \
+                                 capacity, counters, counters + 1};                                           \
+        const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};                                       \
+        return launch_segment_rows<TB, TD>(ov, row_bits, rows, D, keys, src, deltas, sorted, entries, ebits,  \
+                                           unique_out, st);                                                   \
+    }
+    if (dtype == GLSDM_F32 && delta_dtype == GLSDM_F32) GLSDM_OVERLAY(float, float)
+    if (dtype == GLSDM_F32) GLSDM_OVERLAY(float, bf16_t)
+    if (delta_dtype == GLSDM_F32) GLSDM_OVERLAY(bf16_t, float)
+    GLSDM_OVERLAY(bf16_t, bf16_t)
+#undef GLSDM_OVERLAY
 }

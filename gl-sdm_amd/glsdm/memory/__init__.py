@@ -7,6 +7,7 @@ path and are not provided.
 from .state import MemoryView, WriteProposal, DeferredProposal, WriteBuffer, MemoryCache, MemoryBank
 from .transactions import merge, commit
 from .proposals import layer_proposal
+from .overlay import OverlayView
 
 __all__ = ["MemoryView", "WriteProposal", "DeferredProposal", "WriteBuffer", "MemoryCache", "MemoryBank",
-           "merge", "commit", "layer_proposal"]
+           "merge", "commit", "layer_proposal", "OverlayView"]

@@ -284,6 +284,42 @@ int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t D, const in
                              int64_t entries, int32_t width, const float *weights, const float *grad_out,
                              void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * Overlay snapshots: B requests' banks as one immutable base [H, S, D] (dtype)
+ * plus, per request, an int32 slot map [B, H, S] (-1: the base row) into a pool
+ * of touched rows [capacity, D] (dtype).  Logical row (b, h, slot) is
+ * pool[map[b,h,slot]] when mapped, else base[h, slot].  Storage grows with the
+ * touched rows instead of B full replicas, and a commit writes only its touched
+ * rows; every result equals that of the dense [B, H, S, D] bank bit for bit.
+ * Replaces: the per-request clones of S/memory/state.py:61-62 (snapshot) and the
+ * full-bank functional copy of S/memory/transactions.py:96 (commit), following
+ * the overlay plan of P/OPTIMIZATION_PLAN.md:114-120 (P/ = projects/gl-sdm/).
+ */
+
+/* glsdm_read on the logical bank of an overlay. */
+int glsdm_overlay_read(const void *base, int32_t dtype, const int32_t *map, const void *pool, int64_t B,
+                       int64_t H, int64_t S, int64_t D, int64_t T, int32_t width, const int64_t *index,
+                       const float *weights, void *out, int32_t out_dtype, void *stream);
+
+/*
+ * glsdm_commit on the logical bank of an overlay, in place: a touched row's old
+ * value comes from its pool row or the base, its new value goes to its pool
+ * row, allocated on first write (counters[0] = pool rows in use, advanced by
+ * one integer atomic per newly touched row).  A full pool drops that row's
+ * update and sets counters[1] != 0; size the pool for counters[0] + entries.
+ * addresses are absolute rows (b*H + h)*S + slot; keys as glsdm_commit.
+ * Workspace: glsdm_commit_workspace_bytes(entries, B*H*S).
+ */
+int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                         int32_t *map, void *pool, int64_t capacity, uint32_t *counters,
+                         const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                         const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
+                         int64_t *unique_out, void *stream);
+
+/* The logical bank [B, H, S, D] of an overlay, written densely to out. */
+int glsdm_overlay_materialise(const void *base, int32_t dtype, const int32_t *map, const void *pool,
+                              int64_t B, int64_t H, int64_t S, int64_t D, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

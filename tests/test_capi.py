@@ -14,7 +14,8 @@ def test_header_declares_the_expected_surface():
                      "glsdm_commit_workspace_bytes", "glsdm_absolute_addresses", "glsdm_proposal_keys",
                      "glsdm_gather_rows", "glsdm_version", "glsdm_last_error", "glsdm_proposal_error",
                      "glsdm_proposal_delta", "glsdm_commit_proposals", "glsdm_route_backward",
-                     "glsdm_read_backward_weights", "glsdm_read_backward_rows"):
+                     "glsdm_read_backward_weights", "glsdm_read_backward_rows", "glsdm_overlay_read",
+                     "glsdm_overlay_commit", "glsdm_overlay_materialise"):
         assert required in names
 
 
@@ -87,6 +88,17 @@ def test_backward_envelopes():
     assert _rc("glsdm_read_backward_weights", one, 5, 1, 1, 16, 64, 2, 4, one, one, one, None) == N.ERR_ARG
     assert _rc("glsdm_read_backward_rows", one, 16, 4, one, 10, 4, one, one, None, 0, None) == N.ERR_ARG  # 10 % 4
     assert _rc("glsdm_read_backward_rows", one, 16, 4, one, 8, 4, one, one, None, 0, None) == N.ERR_WORKSPACE
+
+
+def test_overlay_envelopes():
+    one = ctypes.c_void_p(16)
+    assert _rc("glsdm_overlay_read", one, 0, one, one, 1, 1, 16, 4096, 2, 4, one, one, one, 0, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_overlay_read", one, 0, None, one, 1, 1, 16, 64, 2, 4, one, one, one, 0, None) == N.ERR_ARG
+    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 1 << 31, one, one, one, 0, None, 8, None, 0,
+               None, None) == N.ERR_UNSUPPORTED                                                     # capacity
+    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 8, one, one, one, 0, None, 8, None, 0,
+               None, None) == N.ERR_WORKSPACE
+    assert _rc("glsdm_overlay_materialise", one, 3, one, one, 1, 1, 16, 4, one, None) == N.ERR_ARG
 
 
 def test_read_and_score_envelopes():
