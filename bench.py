@@ -125,9 +125,10 @@ class Pipeline:
       durations stop being a clean roofline measurement), so it is not the default.
     """
 
-    def __init__(self, cfg, device, write_path="deltas", backward=False):
+    def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False):
         from glsdm import _native as N
         self.N, self.cfg, self.dev, self.write_path, self.backward = N, cfg, device, write_path, backward
+        self.overlay = overlay
         keys, bank, qr, qw, delta = make_inputs(cfg)
         B, T, C, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "C", "H", "half", "dk", "D", "k"))
         self.epochs = T // C
@@ -160,6 +161,14 @@ class Pipeline:
             if write_path == "proposals-materialised":
                 self.rows_buf = torch.empty(B, C, H, k, D, dtype=self.bank.dtype, device=device)
                 self.dbuf = torch.empty(B, C, H, k, D, dtype=torch.float32, device=device)
+        if overlay:
+            if write_path != "deltas" or backward:
+                raise SystemExit("--bank overlay runs the BASELINE protocol only (deltas, no backward)")
+            # one shared base [H, S, D]; per step a fresh request batch: map reset to -1, pool emptied
+            self.base = bank.to(device)
+            self.bank = None
+            self.map = torch.full((B, H, half * half), -1, dtype=torch.int32, device=device)
+            self.pool = torch.empty(self.epochs * self.E, D, dtype=self.base.dtype, device=device)
         if backward:
             # read backward into the learned [H, S, D] bank's fp32 gradient: the
             # requests' replicas fold onto one row (address h*S + slot)
@@ -205,8 +214,19 @@ class Pipeline:
     def memory(self, e, stream, count_unique=False):
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, D, k = (c[x] for x in ("B", "C", "H", "half", "D", "k"))
-        dt = N.dtype_code(self.bank)
+        dt = N.dtype_code(self.base if self.overlay else self.bank)
         uq = p(self.unique) if count_unique else None
+        if self.overlay:
+            dt = N.dtype_code(self.base)
+            S = half * half
+            self._timed("read", stream, lambda: N.call(
+                "glsdm_overlay_read", p(self.base), dt, p(self.map), p(self.pool), B, H, S, D, C, k, p(self.idx[e]),
+                p(self.w[e]), p(self.out), N.F32, st))
+            self._timed("commit", stream, lambda: N.call(
+                "glsdm_overlay_commit", p(self.base), dt, B, H, S, D, p(self.map), p(self.pool),
+                self.pool.shape[0], e * self.E, p(self.addr[e]), p(self.delta[e]), dt, p(self.ckeys[e]),
+                self.E, p(self.ws), self.ws.numel(), uq, st))
+            return
         self._timed("read", stream, lambda: N.call(
             "glsdm_read", p(self.bank), dt, B, H, half * half, D, C, k, p(self.idx[e]), p(self.w[e]),
             p(self.out), N.F32, st))
@@ -253,13 +273,20 @@ class Pipeline:
             "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.dbuf), N.F32,
             p(self.ckeys[e]), self.E, p(self.ws), self.ws.numel(), uq, st))
 
+    def new_batch(self):
+        """Overlay mode: a fresh snapshot of the base for the step's requests (map and pool reset)."""
+        if self.overlay:
+            self.map.fill_(-1)
+
     def step_serial(self):
+        self.new_batch()
         for e in range(self.epochs):
             self.routes(e, self.mem_stream)
             self.memory(e, self.mem_stream)
 
     def step(self):
         rs, ms = self.route_stream, self.mem_stream
+        self.new_batch()
         for e in range(self.epochs):
             rs.wait_event(self.consumed[e])   # the previous step's read/commit of epoch e is done with its routes
             self.routes(e, rs)
@@ -272,7 +299,8 @@ class Pipeline:
     def unique_rows(self):
         """Touched rows U per epoch (untimed serial pass on a scratch copy of the bank)."""
         saved = self.bank
-        self.bank = saved.clone()
+        self.bank = None if self.overlay else saved.clone()
+        self.new_batch()
         out = []
         for e in range(self.epochs):
             self.unique.zero_()
@@ -361,6 +389,9 @@ def main():
                     help="also run the read's backward every epoch: weights' and factor scores' gradients, and "
                          "the bank rows' gradient folded into the learned [H, S, D] bank (reported alongside; "
                          "not the BASELINE protocol)")
+    ap.add_argument("--bank", choices=("dense", "overlay"), default="dense",
+                    help="dense: the per-request replicated bank (default); overlay: one shared base plus each "
+                         "request's touched rows, a fresh batch snapshot per step (map reset instead of a clone)")
     ap.add_argument("--write-path", choices=("deltas", "proposals", "proposals-materialised"), default="deltas",
                     help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
                          "path with the fused proposal commit; proposals-materialised: the same work with "
@@ -378,7 +409,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
-    pipe = Pipeline(cfg, dev, args.write_path, args.backward)
+    pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay")
     unique = pipe.unique_rows()
     for _ in range(args.warmup):
         pipe.step()
@@ -484,10 +515,12 @@ def main():
                                f"D={cfg['D']} k={cfg['k']} {'bf16' if cfg['dtype'] == torch.bfloat16 else 'fp32'}"
                                f"{' Zipf-skewed' if cfg['skew'] else ''}, fused score-route + read + fused "
                                "score-route + keys + " + WRITE_PATHS[args.write_path]
-                               + (" + read backward (route, weights, bank rows)" if args.backward else ""),
+                               + (" + read backward (route, weights, bank rows)" if args.backward else "")
+                               + (" on an overlay bank (shared base + touched rows)" if args.bank == "overlay" else ""),
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],
                    "slots": cfg["half"] ** 2, "key_dim": cfg["dk"], "value_dim": cfg["D"], "top_k": cfg["k"],
-                   "write_path": args.write_path, "backward": args.backward, "parallelism": "single GPU"},
+                   "write_path": args.write_path, "backward": args.backward, "bank": args.bank,
+                   "parallelism": "single GPU"},
         "roofline": roof,
         "read_commit_hbm": {"bytes_per_step": alg_total, "seconds_per_step": rc_time,
                             "achieved_GBps": round(alg_total / rc_time / 1e9, 1),

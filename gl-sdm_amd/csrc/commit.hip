@@ -361,41 +361,32 @@ template <typename TB> struct DenseRows {
     TB *bank;
     int64_t D;
     __device__ __forceinline__ const TB *old_row(int64_t a) const { return bank + a * D; }
-    __device__ __forceinline__ TB *new_row(int64_t a, int, int) const { return bank + a * D; }
+    __device__ __forceinline__ TB *new_row(int64_t a, int, int64_t) const { return bank + a * D; }
 };
 
 // OverlayRows: a shared base [H*S, D] and, per request, a slot map [B*H*S]
-// (-1: the base row) into a pool of rows [capacity, D].  Address
-// a = (b*H + h)*S + slot reads pool row map[a] or base row a % (H*S); its new
-// value goes to its pool row, allocated on first write by one atomic per
-// touched row (pool positions are arbitrary, the values are not).  A full pool
-// drops the row's update and sets *overflow.
+// (-1: the base row) into a pool of rows.  Address a = (b*H + h)*S + slot reads
+// pool row map[a] or base row a % (H*S); a row written for the first time gets
+// pool row offset + p, with p the sorted position of its run's head (distinct
+// per run, < entries), so allocation needs no atomics and the pool layout is
+// the same on every run.  The caller advances offset by entries per commit.
 template <typename TB> struct OverlayRows {
     const TB *base;
     int32_t *map;
     TB *pool;
-    int64_t D, hs, capacity;
-    uint32_t *count, *overflow;
+    int64_t D, hs, offset;
     __device__ __forceinline__ const TB *old_row(int64_t a) const
     {
         const int32_t m = map[a];
         return m >= 0 ? pool + (int64_t)m * D : base + (a % hs) * D;
     }
-    // every lane of the run's group calls it; `li` is the lane within the group,
-    // `first` the group's first lane
-    __device__ __forceinline__ TB *new_row(int64_t a, int li, int first) const
+    // every lane of the run's group calls it; `li` is the lane within the group
+    __device__ __forceinline__ TB *new_row(int64_t a, int li, int64_t head) const
     {
         int32_t m = map[a];
         if (m < 0) {
-            uint32_t r = 0;
-            if (li == 0) r = atomicAdd(count, 1u);
-            r = (uint32_t)__shfl((int)r, first);
-            if ((int64_t)r >= capacity) {
-                if (li == 0) atomicOr(overflow, 1u);
-                return nullptr;
-            }
-            if (li == 0) map[a] = (int32_t)r;
-            m = (int32_t)r;
+            m = (int32_t)(offset + head);
+            if (li == 0) map[a] = m;
         }
         return pool + (int64_t)m * D;
     }
@@ -507,8 +498,7 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
                 last_e = best_e;
             }
         }
-        TB *dst = store.new_row(row_addr, li, lane - li);
-        if (!dst) continue;
+        TB *dst = store.new_row(row_addr, li, p0 + h);
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             const int v = li + c * lpr;
@@ -740,21 +730,23 @@ extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t 
 }
 
 extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
-                                    int32_t *map, void *pool, int64_t capacity, uint32_t *counters,
+                                    int32_t *map, void *pool, int64_t capacity, int64_t pool_offset,
                                     const int64_t *addresses, const void *deltas, int32_t delta_dtype,
                                     const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
                                     int64_t *unique_out, void *stream)
 {
-    if (B < 1 || H < 1 || S < 1 || D < 1 || entries < 0 || capacity < 0)
+    if (B < 1 || H < 1 || S < 1 || D < 1 || entries < 0 || capacity < 0 || pool_offset < 0)
         return fail(GLSDM_ERR_ARG, "overlay_commit: bad shape");
     if (!dtype_ok(dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "overlay_commit: bad dtype");
     if (capacity > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "overlay_commit: capacity above 2^31-1 rows");
     if (entries == 0) return GLSDM_OK;
+    if (pool_offset + entries > capacity)
+        return fail(GLSDM_ERR_ARG, "overlay_commit: pool rows [%lld, %lld) exceed capacity %lld",
+                    (long long)pool_offset, (long long)(pool_offset + entries), (long long)capacity);
     const int64_t rows = B * H * S;
     int rc = check_commit("overlay_commit", rows, D, entries);
     if (rc) return rc;
-    if (!base || !map || !pool || !counters || !addresses || !deltas)
-        return fail(GLSDM_ERR_ARG, "overlay_commit: null pointer");
+    if (!base || !map || !pool || !addresses || !deltas) return fail(GLSDM_ERR_ARG, "overlay_commit: null pointer");
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
@@ -765,7 +757,7 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
 #define GLSDM_OVERLAY(TB, TD)                                                                                  \
     {                                                                                                         \
         const OverlayRows<TB> ov{static_cast<const TB *>(base), map, static_cast<TB *>(pool), D, H * S,       \
-                                 capacity, counters, counters + 1};                                           \
+                                 pool_offset};                                                                \
         const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};                                       \
         return launch_segment_rows<TB, TD>(ov, row_bits, rows, D, keys, src, deltas, sorted, entries, ebits,  \
                                            unique_out, st);                                                   \

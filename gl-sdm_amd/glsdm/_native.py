@@ -39,8 +39,8 @@ SIGNATURES = {
     "glsdm_read_backward_weights": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P], _I32),
     "glsdm_read_backward_rows": ([_P, _I64, _I64, _P, _I64, _I32, _P, _P, _P, _SZ, _P], _I32),
     "glsdm_overlay_read": ([_P, _I32, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _I32, _P], _I32),
-    "glsdm_overlay_commit": ([_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _P, _P, _P, _I32, _P, _I64, _P, _SZ,
-                              _P, _P], _I32),
+    "glsdm_overlay_commit": ([_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _P, _I32, _P, _I64, _P,
+                              _SZ, _P, _P], _I32),
     "glsdm_overlay_materialise": ([_P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "glsdm_commit_proposals": ([_P, _I32, _I64, _I64, _P, _P, _I64, _I32, _P, _P, _P, _P, _I64, _P, _SZ, _P, _P],
                                _I32),

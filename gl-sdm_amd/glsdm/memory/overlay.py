@@ -12,10 +12,11 @@ same bf16 rounding).
 
 Commits update the overlay in place (the stack drops the old view after each
 commit, S/layers/stack.py:65); ``copy()`` gives an independent view at the
-cost of the map and the used pool rows.  Pool capacity is managed on the host
-without a per-commit synchronisation: an upper bound of the rows in use
-(+entries per commit) triggers one read of the device counter, and a larger
-pool only when the true count needs it.
+cost of the map and the used pool rows.  A commit of E entries writes its
+newly touched rows into pool rows [next, next + E) (each at its address run's
+sorted position: no atomics, deterministic layout), so the host knows the
+pool's needs exactly and never synchronises; rows of a run that was already
+mapped are left unused (``mapped_rows()`` counts the live ones).
 """
 from dataclasses import dataclass, field
 
@@ -30,10 +31,9 @@ class OverlayView:
     base: torch.Tensor        # [H, S, D] fp32 or bf16, shared and never written
     map: torch.Tensor         # [B, H, S] int32, -1 = base row
     pool: torch.Tensor        # [capacity, D], same dtype as base
-    counters: torch.Tensor    # [2] int32: rows in use, overflow flag
     version: int = 0
     lineage: object = field(default_factory=object)
-    bound: int = 0            # host upper bound of counters[0]
+    next: int = 0             # first pool row of the next commit
 
     @classmethod
     def from_base(cls, base, batch_size, capacity=None):
@@ -45,32 +45,28 @@ class OverlayView:
         if capacity is None:
             capacity = max(1, min(batch_size * H * S, 1 << 16))
         return cls(base, torch.full((batch_size, H, S), -1, dtype=torch.int32, device=device),
-                   torch.empty(capacity, D, dtype=base.dtype, device=device),
-                   torch.zeros(2, dtype=torch.int32, device=device))
+                   torch.empty(capacity, D, dtype=base.dtype, device=device))
 
     @property
     def shape(self):
         B, H, S = self.map.shape
         return B, H, S, self.base.shape[-1]
 
-    def used(self):
-        """Pool rows in use (synchronises); raises if a commit ever overflowed."""
-        used, overflow = self.counters.tolist()
-        if overflow:
-            raise RuntimeError("overlay pool overflowed: a commit's rows were dropped")
-        self.bound = used
-        return used
+    def pool_rows(self):
+        """Pool rows reserved by the commits so far (host count, no synchronisation)."""
+        return self.next
+
+    def mapped_rows(self):
+        """Rows of the logical bank that differ from the base's storage (synchronises)."""
+        return int((self.map >= 0).sum().item())
 
     def reserve(self, entries):
-        """Make room for a commit of ``entries`` (each touches at most one new row)."""
+        """Grow the pool (doubling) so that the next commit's rows fit."""
         cap = self.pool.shape[0]
-        if self.bound + entries <= cap:
-            return
-        used = self.used()
-        if used + entries > cap:
-            grown = torch.empty(max(2 * cap, used + entries), self.pool.shape[1], dtype=self.pool.dtype,
+        if self.next + entries > cap:
+            grown = torch.empty(max(2 * cap, self.next + entries), self.pool.shape[1], dtype=self.pool.dtype,
                                 device=self.pool.device)
-            grown[:used] = self.pool[:used]
+            grown[:self.next] = self.pool[:self.next]
             self.pool = grown
 
     def read(self, index, weights, out_dtype=torch.float32):
@@ -106,19 +102,18 @@ class OverlayView:
                 workspace = torch.empty(need, dtype=torch.uint8, device=deltas.device)
             deltas = deltas.reshape(E, D).contiguous()
             N.call("glsdm_overlay_commit", N.ptr(self.base), N.dtype_code(self.base), B, H, S, D, N.ptr(self.map),
-                   N.ptr(self.pool), self.pool.shape[0], N.ptr(self.counters), N.ptr(addresses.contiguous()),
+                   N.ptr(self.pool), self.pool.shape[0], self.next, N.ptr(addresses.contiguous()),
                    N.ptr(deltas), N.dtype_code(deltas), N.ptr(None if keys is None else keys.contiguous()), E,
                    N.ptr(workspace), workspace.numel(), N.ptr(unique), N.stream(deltas.device))
-            self.bound += E
+            self.next += E
         self.version += 1
         return self
 
     def copy(self):
-        """An independent view (map and used pool rows copied, base shared)."""
-        used = self.used()
+        """An independent view (map and reserved pool rows copied, base shared)."""
         pool = torch.empty_like(self.pool)
-        pool[:used] = self.pool[:used]
-        return OverlayView(self.base, self.map.clone(), pool, self.counters.clone(), self.version, object(), used)
+        pool[:self.next] = self.pool[:self.next]
+        return OverlayView(self.base, self.map.clone(), pool, self.version, object(), self.next)
 
     def materialise(self):
         """The dense logical bank ``[B, H, S, D]``."""

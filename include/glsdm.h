@@ -304,14 +304,17 @@ int glsdm_overlay_read(const void *base, int32_t dtype, const int32_t *map, cons
 /*
  * glsdm_commit on the logical bank of an overlay, in place: a touched row's old
  * value comes from its pool row or the base, its new value goes to its pool
- * row, allocated on first write (counters[0] = pool rows in use, advanced by
- * one integer atomic per newly touched row).  A full pool drops that row's
- * update and sets counters[1] != 0; size the pool for counters[0] + entries.
- * addresses are absolute rows (b*H + h)*S + slot; keys as glsdm_commit.
+ * row.  A row written for the first time takes pool row pool_offset + p, with p
+ * its address run's position among the sorted entries (no atomics; the pool
+ * layout is deterministic), so each commit uses pool rows
+ * [pool_offset, pool_offset + entries): the caller passes the previous
+ * commit's pool_offset + entries and sizes the pool accordingly
+ * (pool_offset + entries <= capacity, checked).  addresses are absolute rows
+ * (b*H + h)*S + slot; keys as glsdm_commit.
  * Workspace: glsdm_commit_workspace_bytes(entries, B*H*S).
  */
 int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
-                         int32_t *map, void *pool, int64_t capacity, uint32_t *counters,
+                         int32_t *map, void *pool, int64_t capacity, int64_t pool_offset,
                          const int64_t *addresses, const void *deltas, int32_t delta_dtype,
                          const int64_t *keys, int64_t entries, void *workspace, size_t workspace_bytes,
                          int64_t *unique_out, void *stream);

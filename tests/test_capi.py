@@ -94,9 +94,11 @@ def test_overlay_envelopes():
     one = ctypes.c_void_p(16)
     assert _rc("glsdm_overlay_read", one, 0, one, one, 1, 1, 16, 4096, 2, 4, one, one, one, 0, None) == N.ERR_UNSUPPORTED
     assert _rc("glsdm_overlay_read", one, 0, None, one, 1, 1, 16, 64, 2, 4, one, one, one, 0, None) == N.ERR_ARG
-    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 1 << 31, one, one, one, 0, None, 8, None, 0,
+    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 1 << 31, 0, one, one, 0, None, 8, None, 0,
                None, None) == N.ERR_UNSUPPORTED                                                     # capacity
-    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 8, one, one, one, 0, None, 8, None, 0,
+    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 8, 4, one, one, 0, None, 8, None, 0,
+               None, None) == N.ERR_ARG                                                             # 4 + 8 > 8
+    assert _rc("glsdm_overlay_commit", one, 0, 1, 1, 16, 4, one, one, 8, 0, one, one, 0, None, 8, None, 0,
                None, None) == N.ERR_WORKSPACE
     assert _rc("glsdm_overlay_materialise", one, 3, one, one, 1, 1, 16, 4, one, None) == N.ERR_ARG
 

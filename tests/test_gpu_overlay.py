@@ -44,8 +44,8 @@ def test_overlay_matches_dense_over_commits(device, dtype, keyed):
         ov.commit(addr, delta, keys)
         assert ov.version == step + 1
         assert torch.equal(ov.materialise(), dense)
-    assert ov.used() == len(touched)                                       # one pool row per touched row
-    assert ov.pool.shape[0] >= len(touched) > 64                           # the pool grew
+    assert ov.mapped_rows() == len(touched)                                # one pool row per touched row
+    assert ov.pool.shape[0] >= ov.pool_rows() == 4 * 700 > 64              # reserved per commit; the pool grew
     assert torch.equal(base.cpu(), base_before)                            # the base is never written
 
 
@@ -56,7 +56,7 @@ def test_overlay_used_rows_and_copy(device):
     addr = torch.tensor([3, 3, 70, 5, 3, 127], device=device)            # 4 distinct rows of 128
     delta = torch.ones(6, D, device=device)
     ov.commit(addr, delta)
-    assert ov.used() == 4
+    assert ov.mapped_rows() == 4 and ov.pool_rows() == 6
     twin = ov.copy()
     ov.commit(torch.tensor([3], device=device), torch.ones(1, D, device=device))
     dense = twin.materialise()
