@@ -51,10 +51,10 @@ CFG = CONFIGS[2]
 # WRITE x 1.0); source: profiles/glsdm_kernels.config2.hbm-traffic.md.  Re-measured
 # whenever a kernel of the path changes.
 TRAFFIC_PER_LAUNCH = {
-    "score_route": (4964.3 * 1.9998 + 6144.0) * 1024,
-    "read": (67334.2 * 1.9998 + 16384.0) * 1024,
-    "commit": ((10.6 + 2069.0 + 3 * 2534.7 + 133287.6) * 1.9998
-               + (776.1 + 4384.0 + 3 * 4933.5 + 120860.8)) * 1024,
+    "score_route": (5027.2 * 1.9998 + 6144.0) * 1024,
+    "read": (67331.9 * 1.9998 + 16384.0) * 1024,
+    "commit": ((3.1 + 2069.1 + 3 * 2266.1 + 133295.0) * 1.9998
+               + (392.1 + 4672.0 + 3 * 4473.1 + 120860.8)) * 1024,
 }
 
 
