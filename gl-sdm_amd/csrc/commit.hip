@@ -40,6 +40,9 @@ namespace glsdm {
 
 constexpr int RADIX_BITS = 8;
 constexpr int RADIX = 1 << RADIX_BITS;
+#ifndef GLSDM_BUCKET_SORT
+#define GLSDM_BUCKET_SORT 1                              // top-digit pass + per-bucket LDS sort
+#endif
 #ifndef GLSDM_SORT_THREADS
 #define GLSDM_SORT_THREADS 512
 #endif
@@ -68,7 +71,7 @@ constexpr uint32_t LB_SPIN_LIMIT = 1u << 22;            // bounded wait; exceede
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct CommitWorkspace {
-    uint64_t *a, *b;
+    uint64_t *a, *b, *c;
     uint32_t *ghist;    // [MAX_PASSES][RADIX] global digit counts
     uint32_t *status;   // [passes][tiles][RADIX] look-back words
     uint32_t *counter;  // [MAX_PASSES] tile-id counters, then one error word
@@ -89,10 +92,11 @@ static CommitWorkspace plan_workspace(void *base, int64_t entries, int passes)
     char *p = static_cast<char *>(base);
     w.a = reinterpret_cast<uint64_t *>(p);
     w.b = reinterpret_cast<uint64_t *>(p + words);
-    w.ghist = reinterpret_cast<uint32_t *>(p + 2 * words);
-    w.status = reinterpret_cast<uint32_t *>(p + 2 * words + ghist);
-    w.counter = reinterpret_cast<uint32_t *>(p + 2 * words + ghist + status);
-    w.bytes = 2 * words + ghist + status + counter;
+    w.c = reinterpret_cast<uint64_t *>(p + 2 * words);
+    w.ghist = reinterpret_cast<uint32_t *>(p + 3 * words);
+    w.status = reinterpret_cast<uint32_t *>(p + 3 * words + ghist);
+    w.counter = reinterpret_cast<uint32_t *>(p + 3 * words + ghist + status);
+    w.bytes = 3 * words + ghist + status + counter;
     return w;
 }
 
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(256) void commit_prep_kernel(uint32_t *__restrict__
 }
 
 __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ addresses, int64_t rows,
-                                                        int ebits, int passes, int64_t n,
+                                                        int ebits, int first_shift, int passes, int64_t n,
                                                         uint64_t *__restrict__ out, uint32_t *__restrict__ ghist)
 {
     __shared__ uint32_t h[MAX_PASSES][RADIX];
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restric
         const uint64_t v = (row << ebits) | (uint64_t)i;
         out[i] = v;
         for (int p = 0; p < passes; ++p)
-            atomicAdd(&h[p][(uint32_t)(v >> (ebits + p * RADIX_BITS)) & (RADIX - 1)], 1u);
+            atomicAdd(&h[p][(uint32_t)(v >> (first_shift + p * RADIX_BITS)) & (RADIX - 1)], 1u);
     }
     __syncthreads();
     for (int p = 0; p < passes; ++p) {
@@ -268,6 +272,163 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
             const int64_t dst = (int64_t)base[(uint32_t)(x >> shift) & (RADIX - 1)] + j;
             if (dst >= 0 && dst < n) out[dst] = x;   // always in range; the guard keeps a bug from faulting
         }
+    }
+}
+
+// Second step of the address sort when the address needs three or more 8-bit
+// digits: one onesweep pass has grouped the words by their top address digit
+// (256 buckets, stable), and one block per bucket sorts its words by the
+// remaining address digits, least significant first, each pass stable, so the
+// result equals the full LSD sort.  A bucket of up to BK_CAP words is loaded
+// into LDS once and sorted there; a larger one (skewed addresses) is sorted
+// in chunks of BK_CAP through global scratch, with a counting pass per digit.
+constexpr int BK_THREADS = 1024;
+constexpr int BK_ITEMS = 8;
+constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // 8192 words
+constexpr int BK_WAVES = BK_THREADS / 64;
+constexpr int BK_WAVE_ITEMS = BK_CAP / BK_WAVES;       // 512 consecutive words per wave
+
+// Stable ranks of one chunk's items (held BK_ITEMS per thread at wave-major
+// positions): on return (after a block barrier) cnt[w][d] is the number of
+// digit-d items in waves before w, total the chunk's count of digit `tid`
+// (owners), pos[k] the rank of item k among its wave's digit-d items.
+__device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const bool (&valid)[BK_ITEMS], int shift,
+                                        uint32_t (&dig)[BK_ITEMS], uint32_t (&pos)[BK_ITEMS],
+                                        uint32_t (*cnt)[RADIX], uint32_t &total)
+{
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int x = tid; x < BK_WAVES * RADIX; x += BK_THREADS) (&cnt[0][0])[x] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < BK_ITEMS; ++k) {
+        const uint32_t d = (uint32_t)(v[k] >> shift) & (RADIX - 1);
+        dig[k] = d;
+        uint64_t peers = __ballot(valid[k]);
+#pragma unroll
+        for (int bit = 0; bit < RADIX_BITS; ++bit) {
+            const bool on = (d >> bit) & 1u;
+            const uint64_t m = __ballot(on);
+            peers &= on ? m : ~m;
+        }
+        const uint32_t before = (uint32_t)__popcll(peers & lt);
+        uint32_t c = 0;
+        if (valid[k]) c = cnt[wave][d];
+        pos[k] = c + before;
+        if (valid[k] && before == 0) cnt[wave][d] = c + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+    total = 0;
+    if (tid < RADIX) {
+#pragma unroll
+        for (int w = 0; w < BK_WAVES; ++w) {
+            const uint32_t x = cnt[w][tid];
+            cnt[w][tid] = total;
+            total += x;
+        }
+    }
+    __syncthreads();                                      // the wave prefixes are read by every thread
+}
+
+__global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__restrict__ in,
+                                                                 uint64_t *__restrict__ scratch,
+                                                                 uint64_t *__restrict__ out,
+                                                                 const uint32_t *__restrict__ ghist, int ebits,
+                                                                 int lpasses)
+{
+    __shared__ uint64_t s_x[BK_CAP];
+    __shared__ uint64_t s_y[BK_CAP];
+    __shared__ uint32_t cnt[BK_WAVES][RADIX];
+    __shared__ uint32_t lstart[RADIX];
+    __shared__ uint32_t s_wsum[2][RADIX / 64];
+    __shared__ int64_t s_base[RADIX];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int bucket = blockIdx.x;
+    // the bucket's range: exclusive prefix of the top-digit histogram
+    const uint32_t own = tid < RADIX ? ghist[tid] : 0u;
+    const uint32_t excl = digit_scan(own, s_wsum[0]) - own;
+    if (tid == bucket) lstart[0] = excl;
+    __syncthreads();
+    const int64_t start = lstart[0];
+    const int64_t size = ghist[bucket];
+    if (size == 0) return;                                  // block-uniform
+    const int base_at = wave * BK_WAVE_ITEMS + lane;       // item k of this thread: base_at + 64 k
+
+    if (size <= BK_CAP) {
+        // LDS path: load, lpasses stable LDS passes, store
+#pragma unroll
+        for (int k = 0; k < BK_ITEMS; ++k) {
+            const int i = k * BK_THREADS + tid;
+            if (i < size) s_x[i] = in[start + i];
+        }
+        __syncthreads();
+        uint64_t *src = s_x, *dst = s_y;
+        for (int p = 0; p < lpasses; ++p) {
+            uint64_t v[BK_ITEMS];
+            bool valid[BK_ITEMS];
+            uint32_t dig[BK_ITEMS], pos[BK_ITEMS], total;
+#pragma unroll
+            for (int k = 0; k < BK_ITEMS; ++k) {
+                const int i = base_at + 64 * k;
+                valid[k] = i < size;
+                v[k] = valid[k] ? src[i] : 0ull;
+            }
+            bk_rank(v, valid, ebits + p * RADIX_BITS, dig, pos, cnt, total);
+            const uint32_t first = digit_scan(total, s_wsum[p & 1]) - total;
+            if (tid < RADIX) lstart[tid] = first;
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < BK_ITEMS; ++k) {
+                const uint32_t at = lstart[dig[k]] + cnt[wave][dig[k]] + pos[k];
+                if (valid[k] && at < (uint32_t)BK_CAP) dst[at] = v[k];
+            }
+            __syncthreads();
+            uint64_t *t = src; src = dst; dst = t;
+        }
+#pragma unroll
+        for (int k = 0; k < BK_ITEMS; ++k) {
+            const int i = k * BK_THREADS + tid;
+            if (i < size) out[start + i] = src[i];
+        }
+        return;
+    }
+
+    // global path: every pass counts the digits over the bucket, then places its
+    // chunks in order (stable), B -> A -> B ... with the last pass into out
+    uint64_t *src = in + start;
+    for (int p = 0; p < lpasses; ++p) {
+        uint64_t *dst = (p == lpasses - 1) ? out + start : ((p & 1) ? in + start : scratch + start);
+        const int shift = ebits + p * RADIX_BITS;
+        for (int x = tid; x < RADIX; x += BK_THREADS) lstart[x] = 0;
+        __syncthreads();
+        for (int64_t i = tid; i < size; i += BK_THREADS)
+            atomicAdd(&lstart[(uint32_t)(src[i] >> shift) & (RADIX - 1)], 1u);
+        __syncthreads();
+        const uint32_t cnt_d = tid < RADIX ? lstart[tid] : 0u;
+        const uint32_t first = digit_scan(cnt_d, s_wsum[p & 1]) - cnt_d;
+        if (tid < RADIX) s_base[tid] = first;
+        __syncthreads();
+        for (int64_t c0 = 0; c0 < size; c0 += BK_CAP) {
+            uint64_t v[BK_ITEMS];
+            bool valid[BK_ITEMS];
+            uint32_t dig[BK_ITEMS], pos[BK_ITEMS], total;
+#pragma unroll
+            for (int k = 0; k < BK_ITEMS; ++k) {
+                const int64_t i = c0 + base_at + 64 * k;
+                valid[k] = i < size;
+                v[k] = valid[k] ? src[i] : 0ull;
+            }
+            bk_rank(v, valid, shift, dig, pos, cnt, total);
+#pragma unroll
+            for (int k = 0; k < BK_ITEMS; ++k) {
+                const int64_t at = s_base[dig[k]] + cnt[wave][dig[k]] + pos[k];
+                if (valid[k] && at < size) dst[at] = v[k];
+            }
+            __syncthreads();
+            if (tid < RADIX) s_base[tid] += total;
+            __syncthreads();
+        }
+        src = dst;
     }
 }
 
@@ -620,10 +781,28 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
     hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
                        (int64_t)ws.status_words, ws.counter);
     const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), GLSDM_PACK_BLOCKS);
-    hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, passes,
+    int rc;
+#if GLSDM_BUCKET_SORT
+    if (passes >= 3) {
+        // top address digit by one onesweep pass (a -> b), then each bucket by its block (b -> c)
+        const int msd = ebits + abits - RADIX_BITS;
+        hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, msd, 1,
+                           entries, ws.a, ws.ghist);
+        if ((rc = check_launch("commit pack"))) return rc;
+        hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, ws.a, ws.b,
+                           entries, msd, ws.ghist, ws.status, ws.counter, ws.counter + MAX_PASSES);
+        if ((rc = check_launch("onesweep_kernel"))) return rc;
+        hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.a, ws.c, ws.ghist,
+                           ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
+        if ((rc = check_launch("bucket_sort_kernel"))) return rc;
+        *sorted = ws.c;
+        *ebits_out = ebits;
+        return GLSDM_OK;
+    }
+#endif
+    hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, ebits, passes,
                        entries, ws.a, ws.ghist);
-    int rc = check_launch("commit pack");
-    if (rc) return rc;
+    if ((rc = check_launch("commit pack"))) return rc;
 
     uint64_t *src = ws.a, *dst = ws.b;
     for (int p = 0; p < passes; ++p) {

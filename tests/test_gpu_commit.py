@@ -127,3 +127,23 @@ def test_commit_drops_out_of_range_addresses(device):
     keep = bad < 100
     ref, _ = c_oracle.commit(flat, bad[keep], delta[keep])
     assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("keyed", [False, True])
+@pytest.mark.parametrize("rows,D,E,lo,hi", [
+    (1 << 18, 32, 30000, 0, 1 << 18),        # three address digits: top-digit pass + per-bucket LDS sort
+    (1 << 20, 16, 60000, 0, 4096),           # one bucket holds every entry: chunked global bucket sort
+    (1 << 20, 16, 50000, (1 << 20) - 3000, 1 << 20),   # a crowded last bucket plus the out-of-range run
+    ((1 << 17) + 5, 8, 20000, 0, (1 << 17) + 5),
+])
+def test_commit_bucket_sort_paths(device, keyed, rows, D, E, lo, hi):
+    g = torch.Generator().manual_seed(rows + E)
+    flat = torch.randn(rows, D, generator=g)
+    addr = torch.randint(lo, hi, (E,), generator=g)
+    addr[::501] = rows + 7                                  # out of range: dropped
+    delta = torch.randn(E, D, generator=g) * 0.02
+    keys = addr * (E + 1) + torch.randperm(E, generator=g) if keyed else None
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device), None if keys is None else keys.to(device))
+    keep = addr < rows                                      # the oracle takes in-range entries only
+    ref, _ = c_oracle.commit(flat, addr[keep], delta[keep], None if keys is None else keys[keep])
+    assert torch.equal(out.cpu(), ref)
