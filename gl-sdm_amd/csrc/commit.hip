@@ -286,14 +286,13 @@ constexpr int BK_THREADS = 1024;
 constexpr int BK_ITEMS = 8;
 constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // 8192 words
 constexpr int BK_WAVES = BK_THREADS / 64;
-constexpr int BK_WAVE_ITEMS = BK_CAP / BK_WAVES;       // 512 consecutive words per wave
 
 // Stable ranks of one chunk's items (held BK_ITEMS per thread at wave-major
 // positions): on return (after a block barrier) cnt[w][d] is the number of
 // digit-d items in waves before w, total the chunk's count of digit `tid`
 // (owners), pos[k] the rank of item k among its wave's digit-d items.
-__device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const bool (&valid)[BK_ITEMS], int shift,
-                                        uint32_t (&dig)[BK_ITEMS], uint32_t (&pos)[BK_ITEMS],
+__device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const bool (&valid)[BK_ITEMS], int wi,
+                                        int shift, uint32_t (&dig)[BK_ITEMS], uint32_t (&pos)[BK_ITEMS],
                                         uint32_t (*cnt)[RADIX], uint32_t &total)
 {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -302,6 +301,9 @@ __device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const boo
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < BK_ITEMS; ++k) {
+        dig[k] = 0;
+        pos[k] = 0;
+        if (k >= wi) continue;                            // block-uniform: this item slot is empty everywhere
         const uint32_t d = (uint32_t)(v[k] >> shift) & (RADIX - 1);
         dig[k] = d;
         uint64_t peers = __ballot(valid[k]);
@@ -352,9 +354,11 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__res
     const int64_t start = lstart[0];
     const int64_t size = ghist[bucket];
     if (size == 0) return;                                  // block-uniform
-    const int base_at = wave * BK_WAVE_ITEMS + lane;       // item k of this thread: base_at + 64 k
-
     if (size <= BK_CAP) {
+        // wi item slots per thread: each wave takes wi*64 consecutive words, so all
+        // waves share the work and (wave, slot, lane) is still position order
+        const int wi = (int)ceil_div(size, 64 * BK_WAVES);
+        const int base_at = wave * wi * 64 + lane;         // item k of this thread: base_at + 64 k
         // LDS path: load, lpasses stable LDS passes, store
 #pragma unroll
         for (int k = 0; k < BK_ITEMS; ++k) {
@@ -370,10 +374,10 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__res
 #pragma unroll
             for (int k = 0; k < BK_ITEMS; ++k) {
                 const int i = base_at + 64 * k;
-                valid[k] = i < size;
+                valid[k] = k < wi && i < size;
                 v[k] = valid[k] ? src[i] : 0ull;
             }
-            bk_rank(v, valid, ebits + p * RADIX_BITS, dig, pos, cnt, total);
+            bk_rank(v, valid, wi, ebits + p * RADIX_BITS, dig, pos, cnt, total);
             const uint32_t first = digit_scan(total, s_wsum[p & 1]) - total;
             if (tid < RADIX) lstart[tid] = first;
             __syncthreads();
@@ -412,13 +416,16 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__res
             uint64_t v[BK_ITEMS];
             bool valid[BK_ITEMS];
             uint32_t dig[BK_ITEMS], pos[BK_ITEMS], total;
+            const int64_t left = size - c0;
+            const int wi = left < BK_CAP ? (int)ceil_div(left, 64 * BK_WAVES) : BK_ITEMS;
+            const int base_at = wave * wi * 64 + lane;
 #pragma unroll
             for (int k = 0; k < BK_ITEMS; ++k) {
                 const int64_t i = c0 + base_at + 64 * k;
-                valid[k] = i < size;
+                valid[k] = k < wi && i < size;
                 v[k] = valid[k] ? src[i] : 0ull;
             }
-            bk_rank(v, valid, shift, dig, pos, cnt, total);
+            bk_rank(v, valid, wi, shift, dig, pos, cnt, total);
 #pragma unroll
             for (int k = 0; k < BK_ITEMS; ++k) {
                 const int64_t at = s_base[dig[k]] + cnt[wave][dig[k]] + pos[k];
