@@ -372,13 +372,167 @@ def cpu_baseline(cfg, budget_s=12.0):
                       f"scoring + route + read + route + commit, fp32 scalar C oracle, {dt:.1f} s"}
 
 
+# the physical stack (S/layers/stack.py) with
+# 16 distinct layers alternating local (window 512, 16 heads) and global, d_model 1024,
+# head_dim 64 (so 16 memory heads of value dim 64), top-k 16, 512-token clock
+STACK = dict(arch_type="gl_sdm", vocab_size=32000, hidden_size=1024, head_dim=64, num_hidden_layers=16,
+             dtype="bfloat16", gl_layer_pattern=["local", "global"], gl_reads=16, gl_writes=16,
+             gl_chunk_size=512, gl_local_window=512, gl_memory_backend="hip", residual_dtype="float32")
+STACK_CONFIGS = {
+    4: dict(STACK, gl_slots=262144, B=4, T=8192),
+    # 64 streams of a 2^20-slot bank: bf16 request snapshots (64 x 2 GiB)
+    5: dict(STACK, gl_slots=1048576, gl_state_dtype="bfloat16", B=64, prompt=512, decode_steps=4096),
+}
+MEMORY_CALLS = ("routed_snapshot_read", "proposal_keys", "proposal_error", "commit_proposals")
+
+
+def stack_flops_per_token(cfg):
+    """Dense multiply-adds x 2 per token of the stack forward: every Linear once (global
+    layers: q, and k/v/beta/decay/proj for the write path), windowed attention
+    (QK^T and AV over at most `window` keys) and the vocabulary head."""
+    d, V, W = cfg["hidden_size"], cfg["vocab_size"], cfg["gl_local_window"]
+    inner = cfg.get("intermediate_size") or 4 * d
+    H = d // cfg["head_dim"]
+    L = 2 * int(round(cfg["gl_slots"] ** 0.5))
+    mlp = 3 * d * inner
+    local = 5 * d * d + mlp + 2 * W * d
+    glob = 2 * d * H * L + 2 * d * d + 2 * d * H + mlp
+    pattern = cfg["gl_layer_pattern"]
+    n = cfg["num_hidden_layers"]
+    n_global = sum(pattern[i % len(pattern)] == "global" for i in range(n))
+    return 2 * ((n - n_global) * local + n_global * glob + d * V)
+
+
+class CallTimer:
+    """HIP events around the memory operator's entry points (torch's current stream,
+    the stream the library launches on)."""
+
+    def __init__(self, module, names):
+        self.module, self.names, self.orig, self.events = module, names, {}, {}
+
+    def __enter__(self):
+        for n in self.names:
+            f = getattr(self.module, n)
+            self.orig[n] = f
+
+            def wrapped(*a, _f=f, _n=n, **kw):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                out = _f(*a, **kw)
+                e.record()
+                self.events.setdefault(_n, []).append((s, e))
+                return out
+            setattr(self.module, n, wrapped)
+        return self
+
+    def __exit__(self, *exc):
+        for n, f in self.orig.items():
+            setattr(self.module, n, f)
+
+    def totals(self, per):
+        torch.cuda.synchronize()
+        return {n: round(sum(a.elapsed_time(b) for a, b in v) / per, 4) for n, v in self.events.items()}
+
+
+def stack_model(cfg, dev):
+    from glsdm.model import create_model
+    model_cfg = {k: v for k, v in cfg.items() if k not in ("B", "T", "prompt", "decode_steps")}
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = create_model(model_cfg)     # random init, drawn on the device
+    return model.eval()
+
+
+def stack_main(args, dev):
+    from glsdm.memory.backends import hip
+    cfg = STACK_CONFIGS[args.config]
+    model = stack_model(cfg, dev)
+    g = torch.Generator("cpu").manual_seed(0)
+    B = cfg["B"]
+    per_token = stack_flops_per_token(cfg)
+    workload = (f"GL-SDM stack, BASELINE configs[{args.config - 1}]: 16 layers (local window 512 / global) "
+                f"d_model 1024, 16 heads, M={cfg['gl_slots']}, value dim 1024 (16 x 64), top-k 16, clock 512, "
+                f"vocab 32000, bf16 weights, {'fp32' if cfg.get('gl_state_dtype', 'float32') == 'float32' else 'bf16'}"
+                " request snapshots, random init")
+    base = {"metric": "GL-SDM mem-op tokens/s + % HBM roofline (read+commit); full-stack tokens/s",
+            "unit": "tokens/s", "n_gpus": 1, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic (uniform random token ids, seeded; random-init weights)"}
+    if args.config == 4:
+        T = cfg["T"]
+        inputs = torch.randint(cfg["vocab_size"], (B, T), generator=g).to(dev)
+        for _ in range(args.warmup):
+            model.prefill(inputs)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            model.prefill(inputs)
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / args.steps
+        with CallTimer(hip, MEMORY_CALLS) as timer:
+            model.prefill(inputs)
+        mem = timer.totals(1)
+        flops = per_token * B * T
+        result = dict(base, value=round(B * T / (ms * 1e-3), 1), steps=args.steps, warmup=args.warmup,
+                      ms_per_step=round(ms, 3),
+                      config={"workload": workload + "; one step = Model.prefill of the whole batch (new request "
+                              "caches, 16 chunks, 16 commits)", "B": B, "T": T, "layers": 16, "d_model": 1024,
+                              "slots": cfg["gl_slots"], "top_k": 16, "parallelism": "single GPU"},
+                      roofline={"kernel": "whole forward (hipBLASLt GEMMs dominate)", "bound": "mfma",
+                                "achieved": round(flops / (ms * 1e-3) / 1e12, 1), "peak": MFMA_BF16_PEAK / 1e12,
+                                "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
+                                "traffic": None, "flops_per_step": flops},
+                      memory_op_ms_per_step=mem, memory_op_share=round(sum(mem.values()) / ms, 4))
+        print(json.dumps(result))
+        return
+    # config 5: prompt prefill, then one-token decode steps with a commit every 512 tokens
+    P, steps = cfg["prompt"], args.decode_steps or cfg["decode_steps"]
+    prompt = torch.randint(cfg["vocab_size"], (B, P), generator=g).to(dev)
+    tokens = torch.randint(cfg["vocab_size"], (B, steps), generator=g).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    _, cache = model.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    commit_steps = []
+    for s in range(steps):
+        marks[s].record()
+        model.decode(tokens[:, s:s + 1], cache)
+        if cache[0].tokens % cfg["gl_chunk_size"] == 0:
+            commit_steps.append(s)
+    marks[steps].record()
+    torch.cuda.synchronize()
+    dur = [marks[s].elapsed_time(marks[s + 1]) for s in range(steps)]
+    plain = sorted(d for s, d in enumerate(dur) if s not in set(commit_steps))
+    commits = [dur[s] for s in commit_steps]
+    p50 = statistics.median(dur)
+    result = dict(base, value=round(B / (p50 * 1e-3), 1), steps=steps, warmup=0, ms_per_step=round(p50, 4),
+                  higher_is_better=True,
+                  config={"workload": workload + f"; {B} streams, {P}-token prompt, {steps} decode steps of one "
+                          "token per stream, commit every 512 steps", "B": B, "prompt": P, "decode_steps": steps,
+                          "slots": cfg["gl_slots"], "parallelism": "single GPU"},
+                  decode={"p50_ms": round(p50, 4), "p50_ms_without_commit": round(statistics.median(plain), 4),
+                          "p90_ms": round(sorted(dur)[int(0.9 * steps)], 4),
+                          "commit_steps": len(commits),
+                          "commit_step_ms_mean": round(statistics.mean(commits), 3) if commits else None,
+                          "commit_step_ms_max": round(max(commits), 3) if commits else None,
+                          "commit_entries": B * 512 * 8 * 16 * 16, "prefill_s": round(prefill_s, 3)},
+                  roofline=None)
+    print(json.dumps(result))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, choices=(1, 2, 3), default=2,
-                    help="BASELINE.json configs[config-1]; 2 (the headline) is the default")
+    ap.add_argument("--config", type=int, choices=(1, 2, 3, 4, 5), default=2,
+                    help="BASELINE.json configs[config-1]; 2 (the headline) is the default; 4 and 5 run the "
+                         "layer stack (full forward / decode)")
+    ap.add_argument("--decode-steps", type=int, default=None,
+                    help="config 5: decode steps (default 4096, the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--schedule", choices=("serial", "overlap"), default="serial",
                     help="serial: every call on one stream; overlap: routes of later epochs on a second stream")
@@ -408,6 +562,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
+    if args.config in STACK_CONFIGS:
+        stack_main(args, dev)
+        return
     cfg = CONFIGS[args.config]
     pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay")
     unique = pipe.unique_rows()

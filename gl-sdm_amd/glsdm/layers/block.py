@@ -1,0 +1,39 @@
+"""Residual block of the stack's local layers: ``x + attn(norm1(x))`` then
+``x + mlp(norm2(x))`` (S/baselines/block.py:8-27 with the ``transformer``
+mixer, S/ = projects/gl-sdm/src/gl_sdm/)."""
+import torch
+from torch import nn
+
+from .attention import Transformer
+from .common import MLP, RMSNorm
+
+
+def regulariser(x, reg_mode):
+    """The stack's representation regulariser; only ``reg_mode == "baseline"``
+    (zero, S/layers/regularization.py:67-68) is part of the operator build."""
+    del reg_mode
+    return x.new_zeros((), dtype=torch.float32)
+
+
+def check_reg_mode(cfg):
+    if cfg.get("reg_mode", "baseline") != "baseline":
+        raise ValueError("reg_mode must be baseline: the SIGReg sketches are outside the memory-operator build")
+
+
+class Block(nn.Module):
+    def __init__(self, cfg, layer_idx):
+        super().__init__()
+        if cfg["arch_type"] != "transformer":
+            raise ValueError("local layers of the GL-SDM stack use the transformer mixer")
+        check_reg_mode(cfg)
+        self.arch_type = cfg["arch_type"]
+        self.attn = Transformer(cfg, layer_idx)
+        self.norm1, self.norm2 = RMSNorm(cfg["hidden_size"]), RMSNorm(cfg["hidden_size"])
+        self.mlp = MLP(cfg["hidden_size"], cfg.get("intermediate_size"))
+        self.reg_mode = cfg.get("reg_mode", "baseline")
+
+    def forward(self, x, cache=None):
+        dtype = self.mlp.fc.weight.dtype
+        x = x + self.attn(self.norm1(x).to(dtype), cache=cache)
+        x = x + self.mlp(self.norm2(x).to(dtype))
+        return x, regulariser(x, self.reg_mode), x.new_zeros(())

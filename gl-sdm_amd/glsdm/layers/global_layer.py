@@ -1,0 +1,60 @@
+"""One untied global layer: routed read of the chunk snapshot, mixing, MLP,
+and its write proposal (S/layers/global_layer.py:13-54, S/ =
+projects/gl-sdm/src/gl_sdm/)."""
+import torch
+from torch import nn
+import torch.nn.functional as F
+
+from ..memory import routing
+from ..memory.proposals import layer_proposal
+from .block import check_reg_mode, regulariser
+from .common import MLP, RMSNorm
+from .router import GlobalRouter
+
+
+class GlobalLayer(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        check_reg_mode(cfg)
+        dim = cfg["hidden_size"]
+        self.attn = GlobalRouter(cfg)
+        self.norm1, self.norm2 = RMSNorm(dim), RMSNorm(dim)
+        self.mlp = MLP(dim, cfg.get("intermediate_size"))
+        self.reg_mode = cfg.get("reg_mode", "baseline")
+
+    def forward(self, x, snapshot, physical=None):
+        """``x + proj(read_norm(read)) `` then ``+ mlp(norm2(x))``; the read routes
+        ``q(norm1(x))`` (fp32 factor scores) through the snapshot."""
+        B, T, _ = x.shape
+        router = self.attn
+        dtype = router.q.weight.dtype
+        scores = router.q(self.norm1(x).to(dtype)).float().view(B, T, router.heads, -1)
+        readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
+        x = x + router.proj(router.read_norm(readings.to(dtype)).flatten(-2))
+        x = x + self.mlp(self.norm2(x).to(dtype))
+        return x, regulariser(x, self.reg_mode), x.new_zeros(())
+
+    def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None):
+        """Write proposal of the chunk's tokens against ``snapshot``.
+
+        Each token-head's delta against the rows its write route picks is
+        ``(exp(g) - 1) * row + w * beta * (target - exp(g) * prediction)`` with
+        mass 1, with no averaging over tokens or layers; collisions commit in
+        (address, position in chunk, layer) order through the keys.  Outside
+        autograd the deltas stay deferred: the commit forms them from the rows
+        it touches.
+        """
+        if torch.is_grad_enabled() and x.requires_grad:
+            raise NotImplementedError("stack writes are forward-only on the HIP path: run the chunks that "
+                                      "commit under torch.no_grad() or torch.inference_mode()")
+        B, T, _ = x.shape
+        router = self.attn
+        z = self.norm1(x)
+        scores = router.k(z.to(router.k.weight.dtype)).float().view(B, T, router.heads, -1)
+        prediction, index, weights = routing.routed_read(self, snapshot.values, scores, router.num_writes, physical)
+        dense = z.to(router.v.weight.dtype)
+        target = router.v(dense).view(B, T, router.heads, router.head_dim)
+        beta = router.beta(dense).float().sigmoid().unsqueeze(-1)
+        log_decay = -F.softplus(router.decay(dense).float() - 4).unsqueeze(-1)
+        return layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
+                              chunk_size, num_layers)

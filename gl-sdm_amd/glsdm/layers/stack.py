@@ -1,0 +1,78 @@
+"""The physical layer stack and its chunk clock (S/layers/stack.py:12-71,
+S/ = projects/gl-sdm/src/gl_sdm/).
+
+Every layer runs once per chunk of ``gl_chunk_size`` tokens.  All global layers
+read and propose against the chunk-start snapshot (no write is visible between
+layers); at each absolute multiple of the chunk size the pending proposals are
+merged and committed, and local KV history survives the commit.  A request
+cache carries the token count and the proposals of an unfinished chunk across
+prefill/decode calls.  The last chunk of a stateless call proposes nothing.
+
+Outside autograd the commit updates the cache's own snapshot storage in place
+(``gl_commit_in_place``, default on): the snapshot of a chunk is dropped at
+its commit anyway, and a full-bank copy per commit is the cost the fused
+commit exists to avoid.
+"""
+import torch
+
+from ..memory import commit, merge
+from .block import Block
+from .global_layer import GlobalLayer
+
+
+def make_layers(cfg):
+    pattern = cfg["gl_layer_pattern"]
+    count = cfg["num_hidden_layers"]
+    if (not pattern or any(kind not in {"local", "global"} for kind in pattern) or "global" not in pattern
+            or count % len(pattern)):
+        raise ValueError("gl_layer_pattern must include global and repeat to cover num_hidden_layers")
+    if cfg.get("gl_max_steps", 1) != 1 or cfg.get("gl_reasoning", "fixed") != "fixed":
+        raise ValueError("the physical GL-SDM stack has no reasoning loops")
+    if cfg.get("gl_chunk_size", 512) < 1 or cfg.get("gl_local_window", 512) < 1:
+        raise ValueError("positive GL-SDM chunk and local window required")
+    if cfg.get("gl_cuda_graph", False):
+        raise ValueError("physical GL-SDM stack currently uses ordinary training, not legacy loop CUDA graphs")
+    local = {**cfg, "arch_type": "transformer", "attention_window": cfg.get("gl_local_window", 512)}
+    return [GlobalLayer(cfg) if pattern[i % len(pattern)] == "global" else Block(local, i) for i in range(count)]
+
+
+def forward(model, inputs, cache=None):
+    """Run embedded ``inputs [B, T, dim]`` through the stack; returns
+    ``(hidden [B, T, dim], reg, align)``.  ``cache`` is a request cache
+    (``MemoryBank.new_cache``); without one the call is stateless."""
+    B, T, _ = inputs.shape
+    if min(B, T) < 1:
+        raise ValueError("GL-SDM requires a nonempty token batch")
+    retain = cache is not None
+    cache = model.bank.new_cache(B) if cache is None else cache
+    model.bank.validate_cache(cache, B)
+    C = model.cfg.get("gl_chunk_size", 512)
+    layers = len(model.blocks)
+    in_place = model.cfg.get("gl_commit_in_place", True) and not torch.is_grad_enabled()
+    outputs = []
+    reg, align = inputs.new_zeros(()), inputs.new_zeros(())
+    position = 0
+    while position < T:
+        offset = cache.tokens % C
+        length = min(C - offset, T - position)
+        snapshot = cache.view
+        writes = retain or position + length < T
+        proposals = list(cache.pending)
+        x = inputs[:, position:position + length]
+        for i, block in enumerate(model.blocks):
+            if isinstance(block, GlobalLayer):
+                x, r, a = block(x, snapshot)
+                if writes:
+                    proposals.append(block.propose(x, snapshot, offset, i, C, layers))
+            else:
+                x, r, a = block(x, cache.local.setdefault(i, {}))
+            reg, align = reg + r * (length / T), align + a
+        cache.tokens += length
+        if cache.tokens % C == 0 and writes:
+            cache.view = commit(snapshot, merge(snapshot, proposals), donate=in_place)
+            cache.pending = ()
+        else:
+            cache.pending = tuple(proposals)
+        outputs.append(x)
+        position += length
+    return torch.cat(outputs, 1), reg / layers, align / layers

@@ -106,7 +106,9 @@ class MemoryBank(nn.Module):
         return self
 
     def snapshot(self, batch_size):
-        base = self.memory.detach().to(self.state_dtype)
+        # one clone per request; under autograd the reads and commits of the
+        # snapshot carry gradients back to the learned bank (S/memory/state.py:61-62)
+        base = self.memory.to(self.state_dtype)
         return MemoryView(base.unsqueeze(0).expand(batch_size, -1, -1, -1).clone())
 
     def new_cache(self, batch_size):
