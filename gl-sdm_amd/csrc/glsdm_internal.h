@@ -89,6 +89,40 @@ __device__ __forceinline__ uint32_t rank_index(uint64_t key, int tie)
     return tie == GLSDM_TIE_HIGHEST ? lo : 0xFFFFFFFFu - lo;
 }
 
+// 32-bit rank key of a bf16 score: the bf16 order bits (the 16-bit analogue of
+// order_bits: -0 folded onto +0, NaN above +inf) above the 16-bit tie bits of
+// the index (< 65536).  On bf16 values it orders exactly as rank_key does on
+// the same values widened to fp32.
+__device__ __forceinline__ uint32_t rank_key16(bf16_t b, uint32_t index, int tie)
+{
+    uint32_t o;
+    if ((b & 0x7FFFu) > 0x7F80u) o = 0xFFFFu;
+    else if ((b & 0x7FFFu) == 0) o = 0x8000u;
+    else o = (b & 0x8000u) ? (~(uint32_t)b & 0xFFFFu) : ((uint32_t)b | 0x8000u);
+    const uint32_t t = tie == GLSDM_TIE_HIGHEST ? index : 0xFFFFu - index;
+    return (o << 16) | t;
+}
+
+// Score and index of a rank key (64-bit fp32 keys and 32-bit bf16 keys).
+__device__ __forceinline__ float key_value(uint64_t k) { return order_value((uint32_t)(k >> 32)); }
+__device__ __forceinline__ uint32_t key_index(uint64_t k, int tie) { return rank_index(k, tie); }
+__device__ __forceinline__ float key_value(uint32_t k)
+{
+    const uint32_t o = k >> 16;
+    const uint32_t b = (o & 0x8000u) ? (o & 0x7FFFu) : (~o & 0xFFFFu);
+    return __uint_as_float(b << 16);
+}
+__device__ __forceinline__ uint32_t key_index(uint32_t k, int tie)
+{
+    const uint32_t lo = k & 0xFFFFu;
+    return tie == GLSDM_TIE_HIGHEST ? lo : 0xFFFFu - lo;
+}
+// The 64-bit key of the same element (0, the empty-slot sentinel, stays 0).
+__device__ __forceinline__ uint64_t widen_key(uint32_t k, int tie)
+{
+    return k ? rank_key(key_value(k), key_index(k, tie), tie) : 0;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask)
 {
     uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);

@@ -168,20 +168,22 @@ extern "C" int glsdm_read(const void *bank, int32_t bank_dtype, int64_t B, int64
 }
 
 namespace glsdm {
-int route_launch(const float *scores, int64_t rows, int half, int width, int tie, int64_t *index,
-                 float *weights, hipStream_t st);
+int route_launch(const void *scores, int32_t scores_dtype, int64_t rows, int half, int width, int tie,
+                 void *workspace, size_t workspace_bytes, int64_t *index, float *weights, hipStream_t st);
 }
 
 extern "C" int glsdm_route_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S,
-                                int64_t D, int64_t T, const float *scores, int32_t width, int32_t tie,
-                                void *out, int32_t out_dtype, int64_t *index, float *weights, void *stream)
+                                int64_t D, int64_t T, const void *scores, int32_t scores_dtype, int32_t width,
+                                int32_t tie, void *out, int32_t out_dtype, int64_t *index, float *weights,
+                                void *workspace, size_t workspace_bytes, void *stream)
 {
     if (S < 1) return fail(GLSDM_ERR_ARG, "route_read: S must be >= 1");
     int64_t half = 1;
     while (half * half < S) ++half;
     if (half * half != S) return fail(GLSDM_ERR_ARG, "route_read: slots S=%lld is not a square", (long long)S);
     const hipStream_t st = as_stream(stream);
-    int rc = glsdm::route_launch(scores, B * T * H, (int)half, width, tie, index, weights, st);
+    int rc = glsdm::route_launch(scores, scores_dtype, B * T * H, (int)half, width, tie, workspace,
+                                 workspace_bytes, index, weights, st);
     if (rc != GLSDM_OK) return rc;
     return read_launch(bank, bank_dtype, B, H, S, D, T, width, index, weights, out, out_dtype, st);
 }

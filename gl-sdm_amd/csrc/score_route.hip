@@ -330,52 +330,6 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
     }
 }
 
-// One G-lane group per token-head row: merge the per-range lists of each factor,
-// then the candidate stage and the softmax as in score_route_kernel.
-template <int K, int G>
-__global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__restrict__ parts, int64_t rows,
-                                                          int splits, int half, int width, int tie,
-                                                          int64_t *__restrict__ index, float *__restrict__ weights)
-{
-    constexpr int RPB = 256 / G;
-    __shared__ uint32_t s_idx[RPB][2][K];
-    __shared__ float s_val[RPB][2][K];
-    __shared__ uint16_t s_pairs[STAIR_MAX];
-    const int lr = threadIdx.x / G, g = threadIdx.x % G;
-    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
-    const bool live = row < rows;
-    const int64_t r = live ? row : rows - 1;
-    const int kk = width < half ? width : half;
-    const int npairs = staircase_build(s_pairs, kk, width);
-    bool finite = true;
-#pragma unroll
-    for (int f = 0; f < 2; ++f) {
-        uint64_t t[K];
-        if (g < splits) {
-            const uint64_t *src = parts + ((r * 2 + f) * splits + g) * K;
-#pragma unroll
-            for (int w = 0; w < K; ++w) t[w] = src[w];
-        } else {
-            list_clear<K>(t);
-        }
-        for (int s = g + G; s < splits; s += G) {
-            const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
-            uint64_t c[K];
-#pragma unroll
-            for (int w = 0; w < K; ++w) c[w] = src[w];
-            merge_top<K>(t, c);
-        }
-        group_merge<K, G>(t);
-        const bool ok = stash_factor<K, G>(t, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
-        finite = finite && ok;
-    }
-    __syncthreads();
-    uint64_t t[K];
-    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
-                        npairs, finite, t);
-    finish_route<K, G>(t, width, tie, g, live, index + r * width, weights + r * width);
-}
-
 // The split path's shape for (N, H, half, width): 0 splits when the single
 // kernel already fills the GPU (or the split path would not add blocks).
 struct SplitPlan {

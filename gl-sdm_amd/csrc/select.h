@@ -1,4 +1,6 @@
-// Exact top-K selection on 64-bit rank keys, shared by the route kernels.
+// Exact top-K selection on rank keys, shared by the route kernels.  Keys are
+// 64-bit for fp32 scores and 32-bit for bf16 scores (glsdm_internal.h); the
+// list primitives are generic over the key type.
 //
 // A group of G adjacent lanes owns one score row.  Each lane keeps a
 // descending top-K list of keys in registers (K a power of two).  Elements
@@ -26,8 +28,8 @@
 
 namespace glsdm {
 
-template <int K, bool DESC>
-__device__ __forceinline__ void bitonic_sort(uint64_t (&v)[K])
+template <int K, bool DESC, typename KT>
+__device__ __forceinline__ void bitonic_sort(KT (&v)[K])
 {
 #pragma unroll
     for (int size = 2; size <= K; size <<= 1) {
@@ -38,7 +40,7 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&v)[K])
                 const int j = i ^ stride;
                 if (j > i) {
                     const bool down = ((i & size) == 0) == DESC;
-                    const uint64_t a = v[i], b = v[j];
+                    const KT a = v[i], b = v[j];
                     const bool swap = down ? (a < b) : (a > b);
                     v[i] = swap ? b : a;
                     v[j] = swap ? a : b;
@@ -49,8 +51,8 @@ __device__ __forceinline__ void bitonic_sort(uint64_t (&v)[K])
 }
 
 // t <- the K largest of t U c; both sorted descending, result sorted descending.
-template <int K>
-__device__ __forceinline__ void merge_top(uint64_t (&t)[K], const uint64_t (&c)[K])
+template <int K, typename KT>
+__device__ __forceinline__ void merge_top(KT (&t)[K], const KT (&c)[K])
 {
 #pragma unroll
     for (int i = 0; i < K; ++i) t[i] = t[i] > c[K - 1 - i] ? t[i] : c[K - 1 - i];
@@ -60,7 +62,7 @@ __device__ __forceinline__ void merge_top(uint64_t (&t)[K], const uint64_t (&c)[
         for (int i = 0; i < K; ++i) {
             const int j = i ^ stride;
             if (j > i) {
-                const uint64_t a = t[i], b = t[j];
+                const KT a = t[i], b = t[j];
                 t[i] = a > b ? a : b;
                 t[j] = a > b ? b : a;
             }
@@ -68,8 +70,8 @@ __device__ __forceinline__ void merge_top(uint64_t (&t)[K], const uint64_t (&c)[
     }
 }
 
-template <int K>
-__device__ __forceinline__ void list_clear(uint64_t (&t)[K])
+template <int K, typename KT>
+__device__ __forceinline__ void list_clear(KT (&t)[K])
 {
 #pragma unroll
     for (int i = 0; i < K; ++i) t[i] = 0;
@@ -77,21 +79,21 @@ __device__ __forceinline__ void list_clear(uint64_t (&t)[K])
 
 // Sort of 16 keys with the 60-comparator network (bitonic needs 80);
 // descending unless ASC.
-template <bool ASC = false>
-__device__ __forceinline__ void sort16(uint64_t (&v)[16])
+template <bool ASC = false, typename KT>
+__device__ __forceinline__ void sort16(KT (&v)[16])
 {
 #pragma unroll
     for (int c = 0; c < SORTNET16_SIZE; ++c) {
         const int i = SORTNET16[c][0], j = SORTNET16[c][1];
-        const uint64_t a = v[i], b = v[j];
+        const KT a = v[i], b = v[j];
         const bool up = ASC ? a < b : a > b;
         v[i] = up ? a : b;
         v[j] = up ? b : a;
     }
 }
 
-template <int K, bool DESC>
-__device__ __forceinline__ void chunk_sort(uint64_t (&c)[K])
+template <int K, bool DESC, typename KT>
+__device__ __forceinline__ void chunk_sort(KT (&c)[K])
 {
     if constexpr (K == 16)
         sort16<!DESC>(c);
@@ -100,16 +102,16 @@ __device__ __forceinline__ void chunk_sort(uint64_t (&c)[K])
 }
 
 // Merge one unsorted chunk of K keys into the lane's running list.
-template <int K>
-__device__ __forceinline__ void list_absorb(uint64_t (&t)[K], uint64_t (&c)[K])
+template <int K, typename KT>
+__device__ __forceinline__ void list_absorb(KT (&t)[K], KT (&c)[K])
 {
     chunk_sort<K, true>(c);
     merge_top<K>(t, c);
 }
 
 // A lane's first chunk: sorted, it is the list (no merge with an empty list).
-template <int K>
-__device__ __forceinline__ void list_first(uint64_t (&t)[K], uint64_t (&c)[K])
+template <int K, typename KT>
+__device__ __forceinline__ void list_first(KT (&t)[K], KT (&c)[K])
 {
     chunk_sort<K, true>(c);
 #pragma unroll
@@ -118,34 +120,34 @@ __device__ __forceinline__ void list_first(uint64_t (&t)[K], uint64_t (&c)[K])
 
 // Value of lane (lane ^ S) for S in {1, 2} through a DPP quad permute, else a shuffle.
 template <int S>
-__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v)
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v)
 {
-    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    if constexpr (S == 1) {
-        lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
-        hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0xB1, 0xF, 0xF, false);
-    } else if constexpr (S == 2) {
-        lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
-        hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, 0x4E, 0xF, 0xF, false);
-    } else {
-        lo = (uint32_t)__shfl_xor((int)lo, S);
-        hi = (uint32_t)__shfl_xor((int)hi, S);
-    }
-    return ((uint64_t)hi << 32) | lo;
+    if constexpr (S == 1)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    else if constexpr (S == 2)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    else
+        return (uint32_t)__shfl_xor((int)v, S);
 }
 
-template <int K, int S>
-__device__ __forceinline__ void butterfly_level(uint64_t (&t)[K])
+template <int S>
+__device__ __forceinline__ uint64_t lane_xor(uint64_t v)
 {
-    uint64_t p[K];
+    return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
+}
+
+template <int K, int S, typename KT>
+__device__ __forceinline__ void butterfly_level(KT (&t)[K])
+{
+    KT p[K];
 #pragma unroll
-    for (int q = 0; q < K; ++q) p[q] = lane_xor_u64<S>(t[q]);
+    for (int q = 0; q < K; ++q) p[q] = lane_xor<S>(t[q]);
     merge_top<K>(t, p);
 }
 
 // Butterfly merge of the G lane lists of a group (G a power of two <= 64).
-template <int K, int G>
-__device__ __forceinline__ void group_merge(uint64_t (&t)[K])
+template <int K, int G, typename KT>
+__device__ __forceinline__ void group_merge(KT (&t)[K])
 {
     if constexpr (G > 1) butterfly_level<K, 1>(t);
     if constexpr (G > 2) butterfly_level<K, 2>(t);
@@ -156,8 +158,8 @@ __device__ __forceinline__ void group_merge(uint64_t (&t)[K])
 }
 
 // Two independent lists merged level by level (more independent work per level).
-template <int K, int G>
-__device__ __forceinline__ void group_merge2(uint64_t (&t)[K], uint64_t (&u)[K])
+template <int K, int G, typename KT>
+__device__ __forceinline__ void group_merge2(KT (&t)[K], KT (&u)[K])
 {
     if constexpr (G > 1) { butterfly_level<K, 1>(t); butterfly_level<K, 1>(u); }
     if constexpr (G > 2) { butterfly_level<K, 2>(t); butterfly_level<K, 2>(u); }
@@ -169,13 +171,13 @@ __device__ __forceinline__ void group_merge2(uint64_t (&t)[K], uint64_t (&u)[K])
 
 // Exact top-K keys of `n` elements produced by key_of(i), for the G-lane group
 // that lane g belongs to (element i is read by lane i % G).
-template <int K, int G, typename KeyOf>
-__device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (&t)[K])
+template <int K, int G, typename KeyOf, typename KT>
+__device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, KT (&t)[K])
 {
     if constexpr (K >= 32) {
         // at most K/2 elements per lane: sort those, the zero sentinels stay below
         if (n <= G * (K / 2)) {
-            uint64_t c[K / 2];
+            KT c[K / 2];
 #pragma unroll
             for (int q = 0; q < K / 2; ++q) {
                 const int i = q * G + g;
@@ -190,7 +192,7 @@ __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, uint64_t (
     }
     if (n <= 0) list_clear<K>(t);
     for (int base = 0; base < n; base += G * K) {
-        uint64_t c[K];
+        KT c[K];
 #pragma unroll
         for (int q = 0; q < K; ++q) {
             const int i = base + q * G + g;
@@ -323,23 +325,71 @@ __device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, 
 
 // Stashes the top-kk of a factor list (indices and scores) for the candidate
 // stage; returns whether all kk scores are finite.
-template <int K, int G>
-__device__ __forceinline__ bool stash_factor(const uint64_t (&t)[K], int kk, int tie, int g, uint32_t *idx,
+template <int K, int G, typename KT>
+__device__ __forceinline__ bool stash_factor(const KT (&t)[K], int kk, int tie, int g, uint32_t *idx,
                                              float *val)
 {
     bool finite = true;
 #pragma unroll
     for (int i = 0; i < K; ++i) {
         if (i < kk) {
-            const float v = order_value((uint32_t)(t[i] >> 32));
+            const float v = key_value(t[i]);
             finite = finite && (fabsf(v) <= 3.402823466e38f);
             if (i % G == g) {
-                idx[i] = rank_index(t[i], tie);
+                idx[i] = key_index(t[i], tie);
                 val[i] = v;
             }
         }
     }
     return finite;
+}
+
+// Second kernel of the split paths (score_part_kernel, route_part_kernel): one
+// G-lane group per row merges the row's per-range lists of each factor (64-bit
+// keys; each range list holds its range's K best, K >= kk, so the merge is
+// exact), then runs the candidate stage and the softmax.
+template <int K, int G>
+__global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__restrict__ parts, int64_t rows,
+                                                          int splits, int half, int width, int tie,
+                                                          int64_t *__restrict__ index, float *__restrict__ weights)
+{
+    constexpr int RPB = 256 / G;
+    __shared__ uint32_t s_idx[RPB][2][K];
+    __shared__ float s_val[RPB][2][K];
+    __shared__ uint16_t s_pairs[STAIR_MAX];
+    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int64_t row = (int64_t)blockIdx.x * RPB + lr;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;
+    const int kk = width < half ? width : half;
+    const int npairs = staircase_build(s_pairs, kk, width);
+    bool finite = true;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        uint64_t t[K];
+        if (g < splits) {
+            const uint64_t *src = parts + ((r * 2 + f) * splits + g) * K;
+#pragma unroll
+            for (int w = 0; w < K; ++w) t[w] = src[w];
+        } else {
+            list_clear<K>(t);
+        }
+        for (int s = g + G; s < splits; s += G) {
+            const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
+            uint64_t c[K];
+#pragma unroll
+            for (int w = 0; w < K; ++w) c[w] = src[w];
+            merge_top<K>(t, c);
+        }
+        group_merge<K, G>(t);
+        const bool ok = stash_factor<K, G>(t, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
+        finite = finite && ok;
+    }
+    __syncthreads();
+    uint64_t t[K];
+    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
+                        npairs, finite, t);
+    finish_route<K, G>(t, width, tie, g, live, index + r * width, weights + r * width);
 }
 
 }  // namespace glsdm

@@ -22,9 +22,11 @@ _P, _I64, _I32, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_
 SIGNATURES = {
     "glsdm_version": ([], ctypes.c_char_p),
     "glsdm_last_error": ([], ctypes.c_char_p),
-    "glsdm_route": ([_P, _I64, _I32, _I32, _I32, _P, _P, _P], _I32),
+    "glsdm_route": ([_P, _I32, _I64, _I32, _I32, _I32, _P, _P, _P, _SZ, _P], _I32),
+    "glsdm_route_workspace_bytes": ([_I64, _I32, _I32, _P], _I32),
     "glsdm_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _I32, _P], _I32),
-    "glsdm_route_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _P, _I32, _P, _P, _P], _I32),
+    "glsdm_route_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _SZ,
+                          _P], _I32),
     "glsdm_score": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P], _I32),
     "glsdm_score_route": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _SZ, _P], _I32),
     "glsdm_score_route_workspace_bytes": ([_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(_SZ)], _I32),

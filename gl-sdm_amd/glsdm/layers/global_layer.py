@@ -23,12 +23,14 @@ class GlobalLayer(nn.Module):
         self.reg_mode = cfg.get("reg_mode", "baseline")
 
     def forward(self, x, snapshot, physical=None):
-        """``x + proj(read_norm(read)) `` then ``+ mlp(norm2(x))``; the read routes
-        ``q(norm1(x))`` (fp32 factor scores) through the snapshot."""
+        """``x + proj(read_norm(read))`` then ``+ mlp(norm2(x))``; the read routes the
+        factor scores ``q(norm1(x))`` through the snapshot.  The reference widens
+        them with ``.float()`` first; the route takes the projection's bf16 output
+        as is and orders it exactly as its fp32 widening."""
         B, T, _ = x.shape
         router = self.attn
         dtype = router.q.weight.dtype
-        scores = router.q(self.norm1(x).to(dtype)).float().view(B, T, router.heads, -1)
+        scores = router.q(self.norm1(x).to(dtype)).view(B, T, router.heads, -1)
         readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
         x = x + router.proj(router.read_norm(readings.to(dtype)).flatten(-2))
         x = x + self.mlp(self.norm2(x).to(dtype))
@@ -50,7 +52,7 @@ class GlobalLayer(nn.Module):
         B, T, _ = x.shape
         router = self.attn
         z = self.norm1(x)
-        scores = router.k(z.to(router.k.weight.dtype)).float().view(B, T, router.heads, -1)
+        scores = router.k(z.to(router.k.weight.dtype)).view(B, T, router.heads, -1)
         prediction, index, weights = routing.routed_read(self, snapshot.values, scores, router.num_writes, physical)
         dense = z.to(router.v.weight.dtype)
         target = router.v(dense).view(B, T, router.heads, router.head_dim)

@@ -27,6 +27,8 @@ never allocates device memory and never synchronises.  ``route``,
 ``glsdm_read_backward_rows`` and a row gather); the other entry points are
 forward-only and reject inputs that require gradients.
 """
+import ctypes
+
 import torch
 
 from ... import _native as N
@@ -52,6 +54,20 @@ def _square_root(slots):
     return half
 
 
+def route_workspace(rows, half, width, device):
+    """Workspace of the split route path for ``rows`` rows (None when not needed)."""
+    size = ctypes.c_size_t(0)
+    N.call("glsdm_route_workspace_bytes", rows, half, width, ctypes.byref(size))
+    return torch.empty(size.value, dtype=torch.uint8, device=device) if size.value else None
+
+
+def _route_scores(scores):
+    """fp32 or bf16 scores as the kernels take them; bf16 routes exactly as its fp32 widening."""
+    if scores.dtype not in N.DTYPES:
+        scores = scores.float()
+    return scores.contiguous()
+
+
 def _route(scores, count, tie):
     device = require_cuda(scores)
     half = scores.shape[-1] // 2
@@ -60,8 +76,9 @@ def _route(scores, count, tie):
     index = torch.empty((*scores.shape[:-1], count), dtype=torch.int64, device=device)
     weights = torch.empty((*scores.shape[:-1], count), dtype=torch.float32, device=device)
     rows = scores.numel() // scores.shape[-1]
-    N.call("glsdm_route", N.ptr(scores), rows, half, count, N.TIES[tie], N.ptr(index), N.ptr(weights),
-           N.stream(device))
+    ws = route_workspace(rows, half, count, device) if half <= 65535 else None
+    N.call("glsdm_route", N.ptr(scores), N.dtype_code(scores), rows, half, count, N.TIES[tie], N.ptr(index),
+           N.ptr(weights), N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(device))
     return index, weights
 
 
@@ -93,13 +110,13 @@ class _Route(torch.autograd.Function):
 
 
 def route(scores, count, tie="lowest"):
-    """Product-key route of fp32 scores ``[..., 2*half]`` -> (index int64, weights fp32) ``[..., count]``.
+    """Product-key route of fp32 (or bf16) scores ``[..., 2*half]`` -> (index int64, weights fp32)
+    ``[..., count]``; bf16 scores route as their fp32 widening.
 
     Differentiable w.r.t. ``scores`` through the weights (token.py:85-114)."""
-    scores = scores.float().contiguous() if scores.dtype != torch.float32 else scores.contiguous()
     if torch.is_grad_enabled() and scores.requires_grad:
-        return _Route.apply(scores, count, tie)
-    return _route(scores, count, tie)
+        return _Route.apply(scores.float().contiguous(), count, tie)
+    return _route(_route_scores(scores), count, tie)
 
 
 def _read(values, index, weights, out_dtype):
@@ -194,8 +211,10 @@ def _routed_read(values, scores, width, tie, out_dtype):
     out = torch.empty((B, T, H, D), dtype=out_dtype, device=device)
     index = torch.empty((B, T, H, width), dtype=torch.int64, device=device)
     weights = torch.empty((B, T, H, width), dtype=torch.float32, device=device)
-    N.call("glsdm_route_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, N.ptr(scores), width,
-           N.TIES[tie], N.ptr(out), N.dtype_code(out), N.ptr(index), N.ptr(weights), N.stream(device))
+    ws = route_workspace(B * T * H, half, width, device) if half <= 65535 and width <= 64 else None
+    N.call("glsdm_route_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, N.ptr(scores),
+           N.dtype_code(scores), width, N.TIES[tie], N.ptr(out), N.dtype_code(out), N.ptr(index), N.ptr(weights),
+           N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(device))
     return out, index, weights
 
 
@@ -226,7 +245,8 @@ class _RoutedRead(torch.autograd.Function):
 
 def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="highest",
                          out_dtype=torch.float32):
-    """Route fp32 scores ``[B, T, H, 2*half]`` and read the bank ``[B, H, half**2, D]``.
+    """Route fp32 (or bf16) scores ``[B, T, H, 2*half]`` and read the bank ``[B, H, half**2, D]``;
+    bf16 scores route as their fp32 widening.
 
     Returns ``(readings [B,T,H,D], index int64 [B,T,H,width] ascending, weights fp32)``;
     differentiable w.r.t. ``values`` and ``scores`` (through readings and weights).
@@ -234,11 +254,9 @@ def routed_snapshot_read(values, scores, width, allow_large_route=False, tie="hi
     extent up to 65535 is supported.
     """
     del allow_large_route
-    scores = scores if scores.dtype == torch.float32 else scores.float()
-    scores = scores.contiguous()
     if torch.is_grad_enabled() and (values.requires_grad or scores.requires_grad):
-        return _RoutedRead.apply(values, scores, width, tie, out_dtype)
-    return _routed_read(values, scores, width, tie, out_dtype)
+        return _RoutedRead.apply(values, scores.float().contiguous(), width, tie, out_dtype)
+    return _routed_read(values, _route_scores(scores), width, tie, out_dtype)
 
 
 def score(queries, subkeys):

@@ -49,10 +49,16 @@ const char *glsdm_version(void);
 const char *glsdm_last_error(void);
 
 /*
- * Product-key route of fp32 factor scores.
- *   scores  [rows, 2*half] fp32: factor 0 in columns [0, half), factor 1 in [half, 2*half)
+ * Product-key route of fp32 or bf16 factor scores.
+ *   scores  [rows, 2*half] of scores_dtype (GLSDM_F32 or GLSDM_BF16): factor 0 in
+ *           columns [0, half), factor 1 in [half, 2*half).  bf16 scores route exactly
+ *           as the same values widened to fp32 (the reference's .float() of the bf16
+ *           router projection, S/layers/global_layer.py:26,42).
  *   index   [rows, width] int64 out: chosen slots i*half + j, ascending
  *   weights [rows, width] fp32 out: softmax of the chosen slots' summed scores
+ *   workspace (optional, may be NULL): glsdm_route_workspace_bytes() bytes, 8-byte
+ *           aligned; with it, launches of few rows (decode) split each factor's
+ *           columns over more blocks.  Results are identical either way.
  * Per row: per factor the min(width, half) best sub-keys, their grid of fp32
  * sums, the best `width` grid cells, ascending slot order, softmax.
  * Envelope: 1 <= half <= 65535, 1 <= width <= 64, width <= half*half.
@@ -61,8 +67,16 @@ const char *glsdm_last_error(void);
  * S/memory/backends/token.py:85-114 (_Route / route) and S/layers/router.py:39-61, with
  * tie LOWEST.
  */
-int glsdm_route(const float *scores, int64_t rows, int32_t half, int32_t width, int32_t tie,
-                int64_t *index, float *weights, void *stream);
+int glsdm_route(const void *scores, int32_t scores_dtype, int64_t rows, int32_t half, int32_t width,
+                int32_t tie, int64_t *index, float *weights, void *workspace, size_t workspace_bytes,
+                void *stream);
+
+/*
+ * Workspace bytes for glsdm_route / glsdm_route_read on `rows` rows (0 when the
+ * single-kernel path already fills the GPU).  No counterpart in the reference
+ * (its routes allocate internally); sized on the host, no device work.
+ */
+int glsdm_route_workspace_bytes(int64_t rows, int32_t half, int32_t width, size_t *bytes);
 
 /*
  * Snapshot read from supplied routes.
@@ -81,13 +95,15 @@ int glsdm_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64
 
 /*
  * Route then read (glsdm_route followed by glsdm_read on the same stream).
- *   scores [B, T, H, 2*half] fp32 with half*half == S.
+ *   scores [B, T, H, 2*half] of scores_dtype (fp32 or bf16) with half*half == S;
+ *   workspace as glsdm_route, for rows = B*T*H.
  * Replaces: S/memory/backends/urm.py:109-122 (routed_snapshot_read) and
  * S/memory/routing.py:10-28 (torch_routed_read).
  */
 int glsdm_route_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S,
-                     int64_t D, int64_t T, const float *scores, int32_t width, int32_t tie,
-                     void *out, int32_t out_dtype, int64_t *index, float *weights, void *stream);
+                     int64_t D, int64_t T, const void *scores, int32_t scores_dtype, int32_t width,
+                     int32_t tie, void *out, int32_t out_dtype, int64_t *index, float *weights,
+                     void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Address scoring on bf16 MFMA: scores[b,t,h,c] = sum_e queries[b,t,h,e] * subkeys[h,c,e]

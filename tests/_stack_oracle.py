@@ -22,7 +22,8 @@ from glsdm.memory import MemoryView, WriteProposal, routing
 def _routed_read(block, memory, scores, width, physical=None):
     del physical
     device = scores.device
-    out, index, weights = torch_oracle.routed_read(memory.cpu(), scores.cpu(), width, block.attn.tie)
+    # the reference routes the fp32 widening of the projection (S/layers/global_layer.py:26,42)
+    out, index, weights = torch_oracle.routed_read(memory.cpu(), scores.cpu().float(), width, block.attn.tie)
     return out.to(device), index.to(device), weights.to(device)
 
 

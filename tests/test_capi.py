@@ -15,7 +15,7 @@ def test_header_declares_the_expected_surface():
                      "glsdm_gather_rows", "glsdm_version", "glsdm_last_error", "glsdm_proposal_error",
                      "glsdm_proposal_delta", "glsdm_commit_proposals", "glsdm_route_backward",
                      "glsdm_read_backward_weights", "glsdm_read_backward_rows", "glsdm_overlay_read",
-                     "glsdm_overlay_commit", "glsdm_overlay_materialise"):
+                     "glsdm_overlay_commit", "glsdm_overlay_materialise", "glsdm_route_workspace_bytes"):
         assert required in names
 
 
@@ -34,14 +34,30 @@ def _rc(name, *args):
     return getattr(N.lib(), name)(*args)
 
 
+def _route_rc(scores_dtype, rows, half, width, tie):
+    return _rc("glsdm_route", None, scores_dtype, rows, half, width, tie, None, None, None, 0, None)
+
+
 def test_route_rejects_bad_arguments_before_launch():
-    assert _rc("glsdm_route", None, 4, 8, 0, 0, None, None, None) == N.ERR_UNSUPPORTED
-    assert _rc("glsdm_route", None, 4, 8, 65, 0, None, None, None) == N.ERR_UNSUPPORTED
-    assert _rc("glsdm_route", None, 4, 2, 5, 0, None, None, None) == N.ERR_ARG    # width > slots
-    assert _rc("glsdm_route", None, 4, 8, 4, 7, None, None, None) == N.ERR_ARG    # tie
-    assert _rc("glsdm_route", None, 4, 8, 4, 0, None, None, None) == N.ERR_ARG    # null pointers
+    assert _route_rc(0, 4, 8, 0, 0) == N.ERR_UNSUPPORTED
+    assert _route_rc(1, 4, 8, 65, 0) == N.ERR_UNSUPPORTED
+    assert _route_rc(0, 4, 2, 5, 0) == N.ERR_ARG    # width > slots
+    assert _route_rc(0, 4, 8, 4, 7) == N.ERR_ARG    # tie
+    assert _route_rc(5, 4, 8, 4, 0) == N.ERR_ARG    # scores dtype
+    assert _route_rc(1, 4, 8, 4, 0) == N.ERR_ARG    # null pointers
     assert "null" in N.lib().glsdm_last_error().decode()
-    assert _rc("glsdm_route", None, 0, 8, 4, 0, None, None, None) == N.OK         # empty is a no-op
+    assert _route_rc(0, 0, 8, 4, 0) == N.OK         # empty is a no-op
+
+
+def test_route_workspace_contract():
+    """The split path's workspace: sized for few rows (decode), zero when the
+    single-kernel launch already fills the GPU."""
+    size = ctypes.c_size_t(7)
+    assert _rc("glsdm_route_workspace_bytes", 1024, 1024, 16, ctypes.byref(size)) == N.OK
+    assert size.value > 0 and size.value % (1024 * 2 * 16 * 8) == 0
+    assert _rc("glsdm_route_workspace_bytes", 1 << 20, 1024, 16, ctypes.byref(size)) == N.OK
+    assert size.value == 0
+    assert _rc("glsdm_route_workspace_bytes", 1024, 0, 16, ctypes.byref(size)) == N.ERR_ARG
 
 
 def test_commit_workspace_contract():
@@ -107,9 +123,10 @@ def test_read_and_score_envelopes():
     assert _rc("glsdm_read", None, 0, 1, 1, 16, 5000, 1, 4, None, None, None, 0, None) == N.ERR_UNSUPPORTED
     assert _rc("glsdm_score", None, None, 1, 1, 1, 48, 32, None, None) == N.ERR_UNSUPPORTED  # dk % 32
     assert _rc("glsdm_score", None, None, 1, 1, 1, 64, 20, None, None) == N.ERR_UNSUPPORTED  # L % 64
-    assert _rc("glsdm_route_read", None, 0, 1, 1, 15, 8, 1, None, 4, 0, None, 0, None, None, None) == N.ERR_ARG
+    assert _rc("glsdm_route_read", None, 0, 1, 1, 15, 8, 1, None, 0, 4, 0, None, 0, None, None, None, 0,
+               None) == N.ERR_ARG
 
 
 def test_errors_become_python_exceptions():
     with pytest.raises(ValueError, match="width"):
-        N.call("glsdm_route", None, 4, 8, 0, 0, None, None, None)
+        N.call("glsdm_route", None, 0, 4, 8, 0, 0, None, None, None, 0, None)
