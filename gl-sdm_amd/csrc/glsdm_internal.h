@@ -123,6 +123,33 @@ __device__ __forceinline__ uint64_t widen_key(uint32_t k, int tie)
     return k ? rank_key(key_value(k), key_index(k, tie), tie) : 0;
 }
 
+// Factor key of an fp32 score with an index below 65536, as a double: the
+// 48-bit key (order_bits(score) << 16 | 16-bit tie bits) placed at bits
+// [14, 62) above 2^52, i.e. a positive normal double whose numeric order is the
+// key order.  Compare-exchanges of such keys are one v_max_f64 and one
+// v_min_f64 (exact on finite values) instead of a 64-bit compare and four
+// selects; 0.0 is the empty-slot sentinel below every key.
+__device__ __forceinline__ double rank_keyd(float score, uint32_t index, int tie)
+{
+    const uint32_t t = tie == GLSDM_TIE_HIGHEST ? index : 0xFFFFu - index;
+    const uint64_t k48 = ((uint64_t)order_bits(score) << 16) | t;
+    return __longlong_as_double((long long)((1ull << 52) + (k48 << 14)));
+}
+__device__ __forceinline__ uint64_t keyd_bits(double k)
+{
+    return ((uint64_t)__double_as_longlong(k) - (1ull << 52)) >> 14;
+}
+__device__ __forceinline__ float key_value(double k) { return order_value((uint32_t)(keyd_bits(k) >> 16)); }
+__device__ __forceinline__ uint32_t key_index(double k, int tie)
+{
+    const uint32_t lo = (uint32_t)keyd_bits(k) & 0xFFFFu;
+    return tie == GLSDM_TIE_HIGHEST ? lo : 0xFFFFu - lo;
+}
+__device__ __forceinline__ uint64_t widen_key(double k, int tie)
+{
+    return k != 0.0 ? rank_key(key_value(k), key_index(k, tie), tie) : 0;
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask)
 {
     uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);

@@ -5,10 +5,11 @@
 // ranked by a distinct key (monotone score bits above tie bits of its index),
 // which is the total order the reference's chain of stable argsorts induces,
 // so "top-k by key" reproduces the reference's selection exactly, including
-// ties and signed zeros.  fp32 scores use 64-bit keys; bf16 scores (the bf16
-// router projections of the stack, which the reference widens with .float())
-// use 32-bit keys that order exactly as the widened values' 64-bit keys, at a
-// third of the cost per compare-exchange.
+// ties and signed zeros.  fp32 scores use double keys (a 48-bit key as a
+// positive normal double: compare-exchange = v_max_f64 + v_min_f64); bf16
+// scores (the bf16 router projections of the stack, which the reference widens
+// with .float()) use 32-bit keys that order exactly as the widened values'
+// keys (v_max_u32 + v_min_u32).
 //
 // Work decomposition: a group of G adjacent lanes owns one score row.  Each
 // lane keeps a descending top-K list of keys in registers (K = width rounded
@@ -32,8 +33,8 @@ namespace glsdm {
 
 template <typename TS> struct ScoreKey;
 template <> struct ScoreKey<float> {
-    using KT = uint64_t;
-    __device__ __forceinline__ static KT key(float x, uint32_t i, int tie) { return rank_key(x, i, tie); }
+    using KT = double;
+    __device__ __forceinline__ static KT key(float x, uint32_t i, int tie) { return rank_keyd(x, i, tie); }
 };
 template <> struct ScoreKey<bf16_t> {
     using KT = uint32_t;
@@ -179,12 +180,7 @@ __global__ __launch_bounds__(256) void route_part_kernel(const TS *__restrict__ 
         uint64_t *out = parts + ((row * 2 + f) * splits + s) * K;
 #pragma unroll
         for (int w = 0; w < K; ++w) {
-            if (w % G == g) {
-                if constexpr (sizeof(KT) == 8)
-                    out[w] = t[w];
-                else
-                    out[w] = widen_key(t[w], tie);
-            }
+            if (w % G == g) out[w] = widen_key(t[w], tie);
         }
     }
 }

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
 
     bool finite = true;
     for (int fp = 0; fp < 2; fp += NF) {
-        uint64_t ta[K], tb[K];
+        double ta[K], tb[K];
         list_clear<K>(ta);
         if constexpr (PAIR) list_clear<K>(tb);
         // one chunk of CW columns: MFMA scores into LDS, then each lane folds its share
@@ -172,13 +172,13 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
 #pragma unroll
             for (int sub = 0; sub < SUB; ++sub) {
                 const int first = (sub * G + g) * K;
-                uint64_t a[K], b[K];
+                double a[K], b[K];
 #pragma unroll
                 for (int qi = 0; qi < K; ++qi) {
                     const int col = c0 + first + qi;
                     const bool in = col < half;
-                    a[qi] = in ? rank_key(s_sc[0][lr][first + qi], (uint32_t)col, tie) : 0;
-                    if constexpr (PAIR) b[qi] = in ? rank_key(s_sc[NF - 1][lr][first + qi], (uint32_t)col, tie) : 0;
+                    a[qi] = in ? rank_keyd(s_sc[0][lr][first + qi], (uint32_t)col, tie) : 0.0;
+                    if constexpr (PAIR) b[qi] = in ? rank_keyd(s_sc[NF - 1][lr][first + qi], (uint32_t)col, tie) : 0.0;
                 }
                 if (FIRST && sub == 0) {
                     list_first<K>(ta, a);
@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
         if (t < ks) qa[t] = *reinterpret_cast<const bf16x8_t *>(qrow + t * 32);
     const bf16_t *fkeys = keys + ((int64_t)h * L + (int64_t)f * half) * dk;
 
-    uint64_t ta[K];
+    double ta[K];
     list_clear<K>(ta);
     auto chunk = [&](int c0, auto first_tag) {
         constexpr bool FIRST = decltype(first_tag)::value;
@@ -306,11 +306,11 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
             const int first = (sub * G + g) * K;
-            uint64_t a[K];
+            double a[K];
 #pragma unroll
             for (int qi = 0; qi < K; ++qi) {
                 const int col = c0 + first + qi;
-                a[qi] = col < hi ? rank_key(s_sc[lr][first + qi], (uint32_t)col, tie) : 0;
+                a[qi] = col < hi ? rank_keyd(s_sc[lr][first + qi], (uint32_t)col, tie) : 0.0;
             }
             if (FIRST && sub == 0)
                 list_first<K>(ta, a);
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(256) void score_part_kernel(const bf16_t *__restric
         uint64_t *out = parts + (((row_n * H + h) * 2 + f) * splits + s) * K;
 #pragma unroll
         for (int w = 0; w < K; ++w)
-            if (w % G == g) out[w] = ta[w];
+            if (w % G == g) out[w] = widen_key(ta[w], tie);
     }
 }
 

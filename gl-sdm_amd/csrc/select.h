@@ -1,6 +1,7 @@
-// Exact top-K selection on rank keys, shared by the route kernels.  Keys are
-// 64-bit for fp32 scores and 32-bit for bf16 scores (glsdm_internal.h); the
-// list primitives are generic over the key type.
+// Exact top-K selection on rank keys, shared by the route kernels.  Factor keys
+// are doubles for fp32 scores (a 48-bit key as a positive normal double) and
+// 32-bit integers for bf16 scores; candidate keys are 64-bit integers
+// (glsdm_internal.h).  The list primitives are generic over the key type.
 //
 // A group of G adjacent lanes owns one score row.  Each lane keeps a
 // descending top-K list of keys in registers (K a power of two).  Elements
@@ -28,6 +29,15 @@
 
 namespace glsdm {
 
+// Larger / smaller of two distinct keys: v_max_u32 / v_min_u32 for 32-bit keys,
+// v_max_f64 / v_min_f64 for double keys, compare + selects for 64-bit keys.
+__device__ __forceinline__ uint32_t kmax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t kmin(uint32_t a, uint32_t b) { return a > b ? b : a; }
+__device__ __forceinline__ uint64_t kmax(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t kmin(uint64_t a, uint64_t b) { return a > b ? b : a; }
+__device__ __forceinline__ double kmax(double a, double b) { return __builtin_fmax(a, b); }
+__device__ __forceinline__ double kmin(double a, double b) { return __builtin_fmin(a, b); }
+
 template <int K, bool DESC, typename KT>
 __device__ __forceinline__ void bitonic_sort(KT (&v)[K])
 {
@@ -41,9 +51,8 @@ __device__ __forceinline__ void bitonic_sort(KT (&v)[K])
                 if (j > i) {
                     const bool down = ((i & size) == 0) == DESC;
                     const KT a = v[i], b = v[j];
-                    const bool swap = down ? (a < b) : (a > b);
-                    v[i] = swap ? b : a;
-                    v[j] = swap ? a : b;
+                    v[i] = down ? kmax(a, b) : kmin(a, b);
+                    v[j] = down ? kmin(a, b) : kmax(a, b);
                 }
             }
         }
@@ -55,7 +64,7 @@ template <int K, typename KT>
 __device__ __forceinline__ void merge_top(KT (&t)[K], const KT (&c)[K])
 {
 #pragma unroll
-    for (int i = 0; i < K; ++i) t[i] = t[i] > c[K - 1 - i] ? t[i] : c[K - 1 - i];
+    for (int i = 0; i < K; ++i) t[i] = kmax(t[i], c[K - 1 - i]);
 #pragma unroll
     for (int stride = K >> 1; stride > 0; stride >>= 1) {
 #pragma unroll
@@ -63,8 +72,8 @@ __device__ __forceinline__ void merge_top(KT (&t)[K], const KT (&c)[K])
             const int j = i ^ stride;
             if (j > i) {
                 const KT a = t[i], b = t[j];
-                t[i] = a > b ? a : b;
-                t[j] = a > b ? b : a;
+                t[i] = kmax(a, b);
+                t[j] = kmin(a, b);
             }
         }
     }
@@ -86,9 +95,8 @@ __device__ __forceinline__ void sort16(KT (&v)[16])
     for (int c = 0; c < SORTNET16_SIZE; ++c) {
         const int i = SORTNET16[c][0], j = SORTNET16[c][1];
         const KT a = v[i], b = v[j];
-        const bool up = ASC ? a < b : a > b;
-        v[i] = up ? a : b;
-        v[j] = up ? b : a;
+        v[i] = ASC ? kmin(a, b) : kmax(a, b);
+        v[j] = ASC ? kmax(a, b) : kmin(a, b);
     }
 }
 
@@ -134,6 +142,12 @@ template <int S>
 __device__ __forceinline__ uint64_t lane_xor(uint64_t v)
 {
     return ((uint64_t)lane_xor<S>((uint32_t)(v >> 32)) << 32) | lane_xor<S>((uint32_t)v);
+}
+
+template <int S>
+__device__ __forceinline__ double lane_xor(double v)
+{
+    return __longlong_as_double((long long)lane_xor<S>((uint64_t)__double_as_longlong(v)));
 }
 
 template <int K, int S, typename KT>
