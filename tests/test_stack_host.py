@@ -116,3 +116,25 @@ def test_rotary_is_a_rotation_by_absolute_position():
     d0 = (layer.rotary(q, 10) * layer.rotary(k, 7)).sum()
     d1 = (layer.rotary(q, 110) * layer.rotary(k, 107)).sum()
     torch.testing.assert_close(d0, d1, atol=1e-5, rtol=1e-5)
+
+
+
+def test_kv_cache_decode_equals_full_pass():
+    """Hundreds of one-token steps and mixed multi-token calls equal one full
+    pass; the cache keeps exactly the last window - 1 keys."""
+    torch.manual_seed(6)
+    layer = Transformer({**config(), "attention_window": 5}, 0).eval()
+    x = torch.randn(2, 700, 32)
+    with torch.no_grad():
+        full = layer(x)
+        cache = {}
+        out = torch.cat([layer(x[:, :3], cache)] + [layer(x[:, t:t + 1], cache) for t in range(3, 700)], 1)
+        torch.testing.assert_close(out, full, atol=1e-6, rtol=1e-5)
+        assert cache["tokens"] == 700 and cache["k"].shape[2] == 4
+        torch.testing.assert_close(cache["k"], layer.rotary(torch.nn.functional.rms_norm(
+            layer.k(x[:, -4:]).view(2, 4, 2, 16), (16,)), 696).transpose(1, 2))
+        cache, parts, t = {}, [], 0
+        for n in [1, 7, 300, 2, 1, 1, 388]:
+            parts.append(layer(x[:, t:t + n], cache))
+            t += n
+        torch.testing.assert_close(torch.cat(parts, 1), full, atol=1e-6, rtol=1e-5)
