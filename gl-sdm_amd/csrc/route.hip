@@ -151,10 +151,8 @@ __global__ __launch_bounds__(256) void route_kernel(const TS *__restrict__ score
     __syncthreads();
 
     // 2. best `width` cells of the kk x kk grid of fp32 sums, ascending slots, softmax
-    uint64_t t[K];
-    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
-                        npairs, finite, t);
-    finish_route<K, G>(t, width, tie, g, live, index + row * width, weights + row * width);
+    route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
+                     finite, live, index + row * width, weights + row * width);
 }
 
 // One block: 256/G rows, factor f, columns [s*span, s*span + span) of that factor.

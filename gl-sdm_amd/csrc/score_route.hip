@@ -206,11 +206,9 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     }
     chunk_sync<WAVE_LOCAL>();
 
-    uint64_t t[K];
-    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
-                        npairs, finite, t);
     const int64_t out_row = (live ? row_n : 0) * H + h;
-    finish_route<K, G>(t, width, tie, g, live, index + out_row * width, weights + out_row * width);
+    route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
+                     finite, live, index + out_row * width, weights + out_row * width);
 }
 
 // One block: R tokens of head h, factor f, sub-key columns [s*span, s*span + span).

@@ -242,18 +242,52 @@ __device__ __forceinline__ int staircase_build(uint16_t *pairs, int kk, int widt
     return total;
 }
 
+// Keys of the candidate stage (cells of the sum grid): the fp32 sum's order
+// bits above the slot's tie bits.  CellKey64 is the plain 64-bit key;
+// CellKeyD packs the same order into a positive normal double when the slots
+// fit `ib` <= 30 bits (compare-exchange = v_max_f64 + v_min_f64).
+struct CellKey64 {
+    using KT = uint64_t;
+    int tie;
+    __device__ __forceinline__ KT make(float s, uint32_t slot) const { return rank_key(s, slot, tie); }
+    __device__ __forceinline__ uint32_t order(KT k) const { return (uint32_t)(k >> 32); }
+    __device__ __forceinline__ uint32_t slot(KT k) const { return rank_index(k, tie); }
+};
+
+struct CellKeyD {
+    using KT = double;
+    int tie, ib, shift;        // shift = 30 - ib: the 32 + ib key bits end at bit 62
+    uint32_t imask;
+    __device__ __forceinline__ KT make(float s, uint32_t slot) const
+    {
+        const uint32_t t = tie == GLSDM_TIE_HIGHEST ? slot : imask - slot;
+        const uint64_t k = ((uint64_t)order_bits(s) << ib) | t;
+        return __longlong_as_double((long long)((1ull << 52) + (k << shift)));
+    }
+    __device__ __forceinline__ uint64_t raw(KT k) const
+    {
+        return ((uint64_t)__double_as_longlong(k) - (1ull << 52)) >> shift;
+    }
+    __device__ __forceinline__ uint32_t order(KT k) const { return (uint32_t)(raw(k) >> ib); }
+    __device__ __forceinline__ uint32_t slot(KT k) const
+    {
+        const uint32_t t = (uint32_t)raw(k) & imask;
+        return tie == GLSDM_TIE_HIGHEST ? t : imask - t;
+    }
+};
+
 // Best `width` cells (top-K list, descending keys) of the kk x kk sum grid of
 // the factor lists i0/v0 and i1/v1 (sorted descending by rank key).
-template <int K, int G>
+template <int K, int G, typename CK>
 __device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v0, const uint32_t *i1,
-                                              const float *v1, int half, int width, int tie, int g,
+                                              const float *v1, int half, int width, const CK &ck, int g,
                                               const uint16_t *pairs, int npairs, bool finite,
-                                              uint64_t (&t)[K])
+                                              typename CK::KT (&t)[K])
 {
     const int kk = width < half ? width : half;
     auto cell = [&](int i, int j) {
         const float s = v0[i] + v1[j];
-        return rank_key(s, i0[i] * (uint32_t)half + i1[j], tie);
+        return ck.make(s, i0[i] * (uint32_t)half + i1[j]);
     };
     bool exact = false;
     if (finite && npairs >= width) {
@@ -265,7 +299,7 @@ __device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v
         uint32_t tau = 0;
 #pragma unroll
         for (int w = 0; w < K; ++w)
-            if (w == width - 1) tau = (uint32_t)(t[w] >> 32);
+            if (w == width - 1) tau = ck.order(t[w]);
         bool ok = true;
         for (int i = g; i < kk; i += G) {
             const int j = min(kk, width / (i + 1));
@@ -292,17 +326,17 @@ __device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v
 // own (slots are distinct), so no sort is needed.  The max runs over the picks
 // in list order; the exponentials are summed per lane, then across the group by
 // a fixed butterfly, so the result is deterministic.
-template <int K, int G>
-__device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, int tie, int g, bool live,
-                                             int64_t *index_row, float *weight_row)
+template <int K, int G, typename CK>
+__device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], const CK &ck, int width, int g,
+                                             bool live, int64_t *index_row, float *weight_row)
 {
     uint32_t slot[K];
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < K; ++w) {
-        slot[w] = w < width ? rank_index(t[w], tie) : 0xFFFFFFFFu;
+        slot[w] = w < width ? ck.slot(t[w]) : 0xFFFFFFFFu;
         if (w < width) {
-            const float s = order_value((uint32_t)(t[w] >> 32));
+            const float s = order_value(ck.order(t[w]));
             m = (s > m || s != s) ? s : m;
         }
     }
@@ -314,7 +348,7 @@ __device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, 
         const int w = u * G + g;
         e[u] = 0.0f;
         if (w < width && w < K) {
-            e[u] = expf(order_value((uint32_t)(t[w] >> 32)) - m);
+            e[u] = expf(order_value(ck.order(t[w])) - m);
             part += e[u];
         }
     }
@@ -334,6 +368,29 @@ __device__ __forceinline__ void finish_route(const uint64_t (&t)[K], int width, 
                 weight_row[rank] = e[u] * inv;
             }
         }
+    }
+}
+
+// Candidate stage + output stage of one route row from its stashed factor
+// lists: double cell keys when the slots fit 30 bits, else 64-bit keys.
+template <int K, int G>
+__device__ __forceinline__ void route_tail(const uint32_t *i0, const float *v0, const uint32_t *i1, const float *v1,
+                                           int half, int width, int tie, int g, const uint16_t *pairs, int npairs,
+                                           bool finite, bool live, int64_t *index_row, float *weight_row)
+{
+    const int64_t slots = (int64_t)half * half;
+    if (slots <= (1ll << 30)) {
+        int ib = 1;
+        while ((1ll << ib) < slots) ++ib;
+        const CellKeyD ck{tie, ib, 30 - ib, (uint32_t)((1ull << ib) - 1ull)};
+        double t[K];
+        candidate_top<K, G>(i0, v0, i1, v1, half, width, ck, g, pairs, npairs, finite, t);
+        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row);
+    } else {
+        const CellKey64 ck{tie};
+        uint64_t t[K];
+        candidate_top<K, G>(i0, v0, i1, v1, half, width, ck, g, pairs, npairs, finite, t);
+        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row);
     }
 }
 
@@ -400,10 +457,8 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
         finite = finite && ok;
     }
     __syncthreads();
-    uint64_t t[K];
-    candidate_top<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs,
-                        npairs, finite, t);
-    finish_route<K, G>(t, width, tie, g, live, index + r * width, weights + r * width);
+    route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
+                     finite, live, index + r * width, weights + r * width);
 }
 
 }  // namespace glsdm
