@@ -225,10 +225,12 @@ static int launch_route(const TS *scores, int64_t rows, int half, int width, int
                            half, tie, vec, sp.splits, sp.span, parts);
         int rc = check_launch("route_part_kernel");
         if (rc) return rc;
-        // the merge keeps the single kernel's G: the softmax's summation order depends
-        // on the group width, and both paths must give the same bits
-        hipLaunchKernelGGL((route_merge_kernel<K, G>), dim3((unsigned)ceil_div(rows, RPB)), dim3(256), 0, st,
-                           parts, rows, sp.splits, half, width, tie, index, weights);
+        // 16 lanes per row merge the range lists (more blocks for few rows); the
+        // candidate and output stages keep the single kernel's G-lane groups, whose
+        // softmax summation order fixes the bits
+        constexpr int MG = G > 16 ? G : 16;
+        hipLaunchKernelGGL((route_merge_kernel<K, G, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0,
+                           st, parts, rows, sp.splits, half, width, tie, index, weights);
         return check_launch("route_merge_kernel");
     }
     hipLaunchKernelGGL((route_kernel<K, G, (K < 64), TS>), dim3((unsigned)ceil_div(rows, RPB)), dim3(256), 0, st,

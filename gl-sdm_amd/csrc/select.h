@@ -419,16 +419,21 @@ __device__ __forceinline__ bool stash_factor(const KT (&t)[K], int kk, int tie, 
 // G-lane group per row merges the row's per-range lists of each factor (64-bit
 // keys; each range list holds its range's K best, K >= kk, so the merge is
 // exact), then runs the candidate stage and the softmax.
-template <int K, int G>
+template <int K, int G, int MG = G>
 __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__restrict__ parts, int64_t rows,
                                                           int splits, int half, int width, int tie,
                                                           int64_t *__restrict__ index, float *__restrict__ weights)
 {
-    constexpr int RPB = 256 / G;
+    // MG >= G lanes per row merge the range lists; the candidate and output
+    // stages then run in G-lane subgroups (each subgroup computes the same
+    // result; the first one writes it), so the softmax sums in the same order
+    // as a G-lane kernel and the bits do not depend on MG.
+    static_assert(MG >= G && MG % G == 0, "merge group");
+    constexpr int RPB = 256 / MG;
     __shared__ uint32_t s_idx[RPB][2][K];
     __shared__ float s_val[RPB][2][K];
     __shared__ uint16_t s_pairs[STAIR_MAX];
-    const int lr = threadIdx.x / G, g = threadIdx.x % G;
+    const int lr = threadIdx.x / MG, m = threadIdx.x % MG, g = m % G;
     const int64_t row = (int64_t)blockIdx.x * RPB + lr;
     const bool live = row < rows;
     const int64_t r = live ? row : rows - 1;
@@ -438,27 +443,28 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
         uint64_t t[K];
-        if (g < splits) {
-            const uint64_t *src = parts + ((r * 2 + f) * splits + g) * K;
+        if (m < splits) {
+            const uint64_t *src = parts + ((r * 2 + f) * splits + m) * K;
 #pragma unroll
             for (int w = 0; w < K; ++w) t[w] = src[w];
         } else {
             list_clear<K>(t);
         }
-        for (int s = g + G; s < splits; s += G) {
+        for (int s = m + MG; s < splits; s += MG) {
             const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
             uint64_t c[K];
 #pragma unroll
             for (int w = 0; w < K; ++w) c[w] = src[w];
             merge_top<K>(t, c);
         }
-        group_merge<K, G>(t);
-        const bool ok = stash_factor<K, G>(t, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
+        group_merge<K, MG>(t);
+        bool ok = true;
+        if (m < G) ok = stash_factor<K, G>(t, kk, tie, g, s_idx[lr][f], s_val[lr][f]);
         finite = finite && ok;
     }
     __syncthreads();
     route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
-                     finite, live, index + r * width, weights + r * width);
+                     finite, live && m < G, index + r * width, weights + r * width);
 }
 
 }  // namespace glsdm
