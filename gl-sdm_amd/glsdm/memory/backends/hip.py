@@ -76,7 +76,8 @@ def _route(scores, count, tie):
     index = torch.empty((*scores.shape[:-1], count), dtype=torch.int64, device=device)
     weights = torch.empty((*scores.shape[:-1], count), dtype=torch.float32, device=device)
     rows = scores.numel() // scores.shape[-1]
-    ws = route_workspace(rows, half, count, device) if half <= 65535 else None
+    # the split-path workspace only within the route's envelope (outside it the route reports the error)
+    ws = route_workspace(rows, half, count, device) if half <= 65535 and count <= 64 else None
     N.call("glsdm_route", N.ptr(scores), N.dtype_code(scores), rows, half, count, N.TIES[tie], N.ptr(index),
            N.ptr(weights), N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(device))
     return index, weights
