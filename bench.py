@@ -339,6 +339,55 @@ def algorithmic_bytes(cfg, unique, write_path="deltas"):
     return read, read_kernel, [E * D * 4 + E * 16 + x for x in rmw], other
 
 
+def literal_scoring(cfg, dev, reps=20):
+    """The reference's literal scoring projection for one epoch of the workload:
+    ``router.q`` as a bf16 Linear [B*C, d_model] x [d_model, H*L] on hipBLASLt
+    (d_model = H*D, S/layers/global_layer.py:26), and the route of its bf16
+    output as is (glsdm_route, 32-bit keys).  Returns the GEMM's MFMA rate and
+    both calls' times (HIP events on the current stream)."""
+    from glsdm import _native as N
+    from glsdm.memory.backends import hip
+    B, C, H, half, D, k = (cfg[x] for x in ("B", "C", "H", "half", "D", "k"))
+    d_model, L, n = H * D, 2 * half, B * C
+    g = torch.Generator("cpu").manual_seed(5)
+    x = torch.nn.functional.normalize(torch.randn(n, d_model, generator=g), dim=-1).bfloat16().to(dev)
+    # the Linear's weight [H*L, d_model], stored transposed and contiguous for a plain NN product
+    w_t = (torch.randn(H * L, d_model, generator=g) * d_model ** -0.5).bfloat16().t().contiguous().to(dev)
+    scores = torch.empty(n, H * L, dtype=torch.bfloat16, device=dev)
+    index = torch.empty(n * H, k, dtype=torch.int64, device=dev)
+    weights = torch.empty(n * H, k, dtype=torch.float32, device=dev)
+    ws = hip.route_workspace(n * H, half, k, dev)
+    stream = N.stream(dev)
+
+    def gemm():
+        torch.matmul(x, w_t, out=scores)
+
+    def route():
+        N.call("glsdm_route", N.ptr(scores), N.BF16, n * H, half, k, N.TIE_HIGHEST, N.ptr(index),
+               N.ptr(weights), N.ptr(ws), 0 if ws is None else ws.numel(), stream)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    ms_gemm, ms_route = timed(gemm), timed(route)
+    flops = 2 * n * d_model * H * L
+    return {"flops_per_call": flops, "gemm_ms_per_call": round(ms_gemm, 5),
+            "achieved_TFLOPs": round(flops / (ms_gemm * 1e-3) / 1e12, 1),
+            "frac": round(flops / (ms_gemm * 1e-3) / MFMA_BF16_PEAK, 4),
+            "route_ms_per_call": round(ms_route, 5),
+            "shape": f"[{n}, {d_model}] x [{d_model}, {H * L}] bf16 -> bf16 scores, route k={k} over {n * H} rows",
+            "note": "the reference's router.q Linear (hipBLASLt) and the route of its bf16 output, per epoch"}
+
+
 def cpu_baseline(cfg, budget_s=12.0):
     """Scalar C oracle (oracle/glsdm_oracle.c, 1 thread) on a bounded sample of the
     same workload: whole epochs for request 0, repeated until ~budget_s."""
@@ -693,6 +742,8 @@ def main():
         "calls_per_step": calls,
         "unique_rows_per_epoch": unique,
     }
+    if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense":
+        result["literal_scoring_mfma"] = literal_scoring(cfg, dev)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
