@@ -51,7 +51,7 @@ constexpr int SORT_THREADS = GLSDM_SORT_THREADS;       // >= RADIX: threads belo
 #define GLSDM_SORT_ITEMS 8
 #endif
 #ifndef GLSDM_PACK_BLOCKS
-#define GLSDM_PACK_BLOCKS 256
+#define GLSDM_PACK_BLOCKS 1024
 #endif
 constexpr int SORT_ITEMS = GLSDM_SORT_ITEMS;            // per thread
 constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // entries per tile
