@@ -6,9 +6,10 @@ factor scores per head), key dim dk=128, value dim D=128 (H*D = 1024), top-k
 16, bf16 bank/queries/deltas, fp32 accumulation.  One step = all 4 epochs of:
 
   score+route(read queries) -> snapshot read               (read path)
-  score+route(write queries) -> proposal keys -> commit     (write path)
+  score+route+keys(write queries) -> commit                 (write path)
 
-(score+route is one fused kernel: MFMA scores feed the top-k through LDS)
+(score+route is one fused kernel: MFMA scores feed the top-k through LDS; the
+write route's kernel also emits the proposal addresses and collision keys)
 
 with the bank updated in place at every 512-token clock (donated commit).
 ``--write-path proposals`` replaces the synthetic deltas by the stack's write
@@ -204,12 +205,11 @@ class Pipeline:
         self._timed("score_route", stream, lambda: N.call(
             "glsdm_score_route", p(self.qr[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, None,
             p(self.idx[e]), p(self.w[e]), p(self.route_ws), self.route_ws.numel(), st))
-        self._timed("score_route", stream, lambda: N.call(
-            "glsdm_score_route", p(self.qw[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, None,
-            p(self.widx[e]), p(self.ww[e]), p(self.route_ws), self.route_ws.numel(), st))
-        self._timed("keys", stream, lambda: N.call(
-            "glsdm_proposal_keys", p(self.widx[e]), B, C, H, k, half * half, 0, C, 1, 0,
-            p(self.addr[e]), p(self.ckeys[e]), st))
+        # the write route also emits its proposal addresses and keys addr*C + t (one launch)
+        self._timed("score_route_keys", stream, lambda: N.call(
+            "glsdm_score_route_keys", p(self.qw[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, 0, C, 1, 0,
+            p(self.widx[e]), p(self.ww[e]), p(self.addr[e]), p(self.ckeys[e]), p(self.route_ws),
+            self.route_ws.numel(), st))
 
     def memory(self, e, stream, count_unique=False):
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
@@ -723,7 +723,7 @@ def main():
                                f"({epochs} epochs of {cfg['C']}) H={cfg['H']} M={cfg['half'] ** 2} dk={cfg['dk']} "
                                f"D={cfg['D']} k={cfg['k']} {'bf16' if cfg['dtype'] == torch.bfloat16 else 'fp32'}"
                                f"{' Zipf-skewed' if cfg['skew'] else ''}, fused score-route + read + fused "
-                               "score-route + keys + " + WRITE_PATHS[args.write_path]
+                               "score-route-keys + " + WRITE_PATHS[args.write_path]
                                + (" + read backward (route, weights, bank rows)" if args.backward else "")
                                + (" on an overlay bank (shared base + touched rows)" if args.bank == "overlay" else ""),
                    "B": cfg["B"], "T": cfg["T"], "chunk": cfg["C"], "heads": cfg["H"],

@@ -230,7 +230,7 @@ static int launch_route(const TS *scores, int64_t rows, int half, int width, int
         // softmax summation order fixes the bits
         constexpr int MG = G > 16 ? G : 16;
         hipLaunchKernelGGL((route_merge_kernel<K, G, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0,
-                           st, parts, rows, sp.splits, half, width, tie, index, weights);
+                           st, parts, rows, sp.splits, half, width, tie, index, weights, KeyArgs{}, (int64_t)1);
         return check_launch("route_merge_kernel");
     }
     hipLaunchKernelGGL((route_kernel<K, G, (K < 64), TS>), dim3((unsigned)ceil_div(rows, RPB)), dim3(256), 0, st,

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
                                                           int64_t H, int dk, int half, int width, int tie,
                                                           float *__restrict__ scores_out,
                                                           int64_t *__restrict__ index,
-                                                          float *__restrict__ weights)
+                                                          float *__restrict__ weights, KeyArgs ka)
 {
     constexpr int R = 256 / G;       // tokens per block
     constexpr int RT = R / 16;       // 16-row MFMA tiles
@@ -207,8 +207,9 @@ __global__ __launch_bounds__(256) void score_route_kernel(const bf16_t *__restri
     chunk_sync<WAVE_LOCAL>();
 
     const int64_t out_row = (live ? row_n : 0) * H + h;
+    const KeyRow kr = ka.addr ? key_row(ka, out_row, H, width) : KeyRow{nullptr, nullptr, 0, 0, 0};
     route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
-                     finite, live, index + out_row * width, weights + out_row * width);
+                     finite, live, index + out_row * width, weights + out_row * width, kr);
 }
 
 // One block: R tokens of head h, factor f, sub-key columns [s*span, s*span + span).
@@ -360,7 +361,7 @@ static SplitPlan split_plan(int64_t N, int64_t H, int half, int width)
 template <int K>
 static int launch_split(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half, int width,
                         int tie, const SplitPlan &p, float *scores_out, uint64_t *parts, int64_t *index,
-                        float *weights, hipStream_t st)
+                        float *weights, const KeyArgs &ka, hipStream_t st)
 {
     constexpr int G = 4;
     constexpr int CW = K <= 16 ? 64 : 4 * K;
@@ -379,14 +380,14 @@ static int launch_split(const void *q, const void *keys, int64_t N, int64_t H, i
     constexpr int MG = K >= 32 ? 8 : 4;
     const int64_t rows = N * H;
     hipLaunchKernelGGL((route_merge_kernel<K, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0, st,
-                       parts, rows, p.splits, half, width, tie, index, weights);
+                       parts, rows, p.splits, half, width, tie, index, weights, ka, H);
     return check_launch("route_merge_kernel");
 }
 
 template <int K, int G, int CW, bool PAIR>
 static int launch_score_route(const void *q, const void *keys, int64_t N, int64_t H, int dk, int half,
                               int width, int tie, float *scores_out, int64_t *index, float *weights,
-                              hipStream_t st)
+                              const KeyArgs &ka, hipStream_t st)
 {
     constexpr int R = 256 / G;
     const int64_t blocks = ceil_div(N, R) * H;
@@ -395,10 +396,10 @@ static int launch_score_route(const void *q, const void *keys, int64_t N, int64_
     constexpr bool STAGE = K <= 16;   // the larger lists need the LDS for themselves
     if (dk <= 128)
         hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR, 4, STAGE>), dim3((unsigned)blocks), dim3(256), 0,
-                           st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights);
+                           st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights, ka);
     else
         hipLaunchKernelGGL((score_route_kernel<K, G, CW, PAIR, KS_MAX, STAGE>), dim3((unsigned)blocks),
-                           dim3(256), 0, st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights);
+                           dim3(256), 0, st, qq, kk, N, H, dk, half, width, tie, scores_out, index, weights, ka);
     return check_launch("score_route_kernel");
 }
 
@@ -416,10 +417,10 @@ extern "C" int glsdm_score_route_workspace_bytes(int64_t B, int64_t T, int64_t H
     return GLSDM_OK;
 }
 
-extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
-                                 int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
-                                 int64_t *index, float *weights, void *workspace, size_t workspace_bytes,
-                                 void *stream)
+static int score_route_any(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H, int32_t dk,
+                           int32_t half, int32_t width, int32_t tie, float *scores_out, int64_t *index,
+                           float *weights, const KeyArgs &ka, void *workspace, size_t workspace_bytes,
+                           hipStream_t st)
 {
     if (B < 0 || T < 0 || H < 1 || dk < 1 || half < 1) return fail(GLSDM_ERR_ARG, "score_route: bad shape");
     if (dk % 32 != 0 || dk > 32 * KS_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "score_route: dk=%d must be a multiple of 32 up to 256", dk);
@@ -432,28 +433,50 @@ extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64
     if (!queries || !subkeys || !index || !weights) return fail(GLSDM_ERR_ARG, "score_route: null pointer");
     if (((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(subkeys)) & 15) != 0)
         return fail(GLSDM_ERR_UNSUPPORTED, "score_route: queries and sub-keys must be 16-byte aligned");
-    const hipStream_t st = as_stream(stream);
     const SplitPlan plan = split_plan(N, H, half, width);
     if (plan.splits > 0 && workspace && workspace_bytes >= plan.bytes &&
         (reinterpret_cast<uintptr_t>(workspace) & 7) == 0) {
         uint64_t *parts = static_cast<uint64_t *>(workspace);
         switch (pow2_ceil(width)) {
-        case 1: return launch_split<1>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        case 2: return launch_split<2>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        case 4: return launch_split<4>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        case 8: return launch_split<8>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        case 16: return launch_split<16>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        case 32: return launch_split<32>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
-        default: return launch_split<64>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, st);
+        case 1: return launch_split<1>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        case 2: return launch_split<2>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        case 4: return launch_split<4>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        case 8: return launch_split<8>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        case 16: return launch_split<16>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        case 32: return launch_split<32>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
+        default: return launch_split<64>(queries, subkeys, N, H, dk, half, width, tie, plan, scores_out, parts, index, weights, ka, st);
         }
     }
     switch (pow2_ceil(width)) {
-    case 1: return launch_score_route<1, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 2: return launch_score_route<2, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 4: return launch_score_route<4, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 8: return launch_score_route<8, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 16: return launch_score_route<16, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    case 32: return launch_score_route<32, 8, 256, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
-    default: return launch_score_route<64, 8, 512, false>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, st);
+    case 1: return launch_score_route<1, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    case 2: return launch_score_route<2, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    case 4: return launch_score_route<4, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    case 8: return launch_score_route<8, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    case 16: return launch_score_route<16, 4, 64, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    case 32: return launch_score_route<32, 8, 256, true>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
+    default: return launch_score_route<64, 8, 512, false>(queries, subkeys, N, H, dk, half, width, tie, scores_out, index, weights, ka, st);
     }
+}
+
+extern "C" int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                                 int32_t dk, int32_t half, int32_t width, int32_t tie, float *scores_out,
+                                 int64_t *index, float *weights, void *workspace, size_t workspace_bytes,
+                                 void *stream)
+{
+    return score_route_any(queries, subkeys, B, T, H, dk, half, width, tie, scores_out, index, weights, KeyArgs{},
+                           workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int glsdm_score_route_keys(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                                      int32_t dk, int32_t half, int32_t width, int32_t tie, int64_t position_offset,
+                                      int64_t chunk, int64_t layers, int64_t layer, int64_t *index, float *weights,
+                                      int64_t *addresses, int64_t *keys, void *workspace, size_t workspace_bytes,
+                                      void *stream)
+{
+    if (chunk < 1 || layers < 1 || layer < 0 || layer >= layers || position_offset < 0)
+        return fail(GLSDM_ERR_ARG, "score_route_keys: bad key arguments");
+    if (B * T > 0 && (!addresses || !keys)) return fail(GLSDM_ERR_ARG, "score_route_keys: null pointer");
+    const KeyArgs ka{addresses, keys, T, (int64_t)half * half, position_offset, chunk, layers, layer};
+    return score_route_any(queries, subkeys, B, T, H, dk, half, width, tie, nullptr, index, weights, ka, workspace,
+                           workspace_bytes, as_stream(stream));
 }

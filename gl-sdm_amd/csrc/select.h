@@ -242,6 +242,28 @@ __device__ __forceinline__ int staircase_build(uint16_t *pairs, int kk, int widt
     return total;
 }
 
+// Optional proposal-key outputs of a route (glsdm_score_route_keys): for row
+// (request b, position t, head h) the pick of slot s gets the absolute address
+// a = (b*H + h)*S + s and the collision key a*chunk*layers + (offset + t)*layers
+// + layer, at its output position (the arithmetic of glsdm_proposal_keys).
+struct KeyArgs {
+    int64_t *addr, *keys;        // [rows, width] each; addr == nullptr: no key outputs
+    int64_t T, S, offset, chunk, layers, layer;
+};
+
+struct KeyRow {
+    int64_t *addr, *keys;
+    int64_t base, mul, add;
+};
+
+// The key outputs of flattened route row r = (b*T + t)*H + h.
+__device__ __forceinline__ KeyRow key_row(const KeyArgs &ka, int64_t r, int64_t H, int width)
+{
+    const int64_t h = r % H, bt = r / H, t = bt % ka.T, b = bt / ka.T;
+    return KeyRow{ka.addr + r * width, ka.keys + r * width, (b * H + h) * ka.S, ka.chunk * ka.layers,
+                  (ka.offset + t) * ka.layers + ka.layer};
+}
+
 // Keys of the candidate stage (cells of the sum grid): the fp32 sum's order
 // bits above the slot's tie bits.  CellKey64 is the plain 64-bit key;
 // CellKeyD packs the same order into a positive normal double when the slots
@@ -328,7 +350,8 @@ __device__ __forceinline__ void candidate_top(const uint32_t *i0, const float *v
 // a fixed butterfly, so the result is deterministic.
 template <int K, int G, typename CK>
 __device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], const CK &ck, int width, int g,
-                                             bool live, int64_t *index_row, float *weight_row)
+                                             bool live, int64_t *index_row, float *weight_row,
+                                             const KeyRow &kr)
 {
     uint32_t slot[K];
     float m = -INFINITY;
@@ -366,6 +389,11 @@ __device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], cons
                 for (int j = 0; j < K; ++j) rank += slot[j] < slot[w] ? 1 : 0;
                 index_row[rank] = (int64_t)slot[w];
                 weight_row[rank] = e[u] * inv;
+                if (kr.addr) {
+                    const int64_t a = kr.base + (int64_t)slot[w];
+                    kr.addr[rank] = a;
+                    kr.keys[rank] = a * kr.mul + kr.add;
+                }
             }
         }
     }
@@ -376,7 +404,8 @@ __device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], cons
 template <int K, int G>
 __device__ __forceinline__ void route_tail(const uint32_t *i0, const float *v0, const uint32_t *i1, const float *v1,
                                            int half, int width, int tie, int g, const uint16_t *pairs, int npairs,
-                                           bool finite, bool live, int64_t *index_row, float *weight_row)
+                                           bool finite, bool live, int64_t *index_row, float *weight_row,
+                                           const KeyRow &kr = KeyRow{nullptr, nullptr, 0, 0, 0})
 {
     const int64_t slots = (int64_t)half * half;
     if (slots <= (1ll << 30)) {
@@ -385,12 +414,12 @@ __device__ __forceinline__ void route_tail(const uint32_t *i0, const float *v0, 
         const CellKeyD ck{tie, ib, 30 - ib, (uint32_t)((1ull << ib) - 1ull)};
         double t[K];
         candidate_top<K, G>(i0, v0, i1, v1, half, width, ck, g, pairs, npairs, finite, t);
-        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row);
+        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row, kr);
     } else {
         const CellKey64 ck{tie};
         uint64_t t[K];
         candidate_top<K, G>(i0, v0, i1, v1, half, width, ck, g, pairs, npairs, finite, t);
-        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row);
+        finish_route<K, G>(t, ck, width, g, live, index_row, weight_row, kr);
     }
 }
 
@@ -422,7 +451,8 @@ __device__ __forceinline__ bool stash_factor(const KT (&t)[K], int kk, int tie, 
 template <int K, int G, int MG = G>
 __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__restrict__ parts, int64_t rows,
                                                           int splits, int half, int width, int tie,
-                                                          int64_t *__restrict__ index, float *__restrict__ weights)
+                                                          int64_t *__restrict__ index, float *__restrict__ weights,
+                                                          KeyArgs ka, int64_t heads)
 {
     // MG >= G lanes per row merge the range lists; the candidate and output
     // stages then run in G-lane subgroups (each subgroup computes the same
@@ -463,8 +493,9 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
         finite = finite && ok;
     }
     __syncthreads();
+    const KeyRow kr = ka.addr ? key_row(ka, r, heads, width) : KeyRow{nullptr, nullptr, 0, 0, 0};
     route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
-                     finite, live && m < G, index + r * width, weights + r * width);
+                     finite, live && m < G, index + r * width, weights + r * width, kr);
 }
 
 }  // namespace glsdm

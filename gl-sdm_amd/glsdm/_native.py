@@ -29,6 +29,8 @@ SIGNATURES = {
                           _P], _I32),
     "glsdm_score": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P], _I32),
     "glsdm_score_route": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _SZ, _P], _I32),
+    "glsdm_score_route_keys": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _P, _P,
+                                _P, _P, _P, _SZ, _P], _I32),
     "glsdm_score_route_workspace_bytes": ([_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(_SZ)], _I32),
     "glsdm_commit_workspace_bytes": ([_I64, _I64, ctypes.POINTER(_SZ)], _I32),
     "glsdm_commit": ([_P, _I32, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),

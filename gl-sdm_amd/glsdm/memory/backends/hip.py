@@ -312,6 +312,37 @@ def score_route(queries, subkeys, width, tie="highest", export_scores=False, spl
     return index, weights, scores
 
 
+def score_route_keys(queries, subkeys, width, offset, chunk_size, num_layers, layer_idx, tie="highest",
+                     split=True, workspace=None):
+    """Fused scoring + route + proposal keys: ``(index, weights, addresses, keys)``,
+    each ``[B, T, H, width]``; equal to :func:`score_route` followed by
+    :func:`proposal_keys` (forward-only)."""
+    _no_grad(queries, subkeys)
+    device = require_cuda(queries, subkeys)
+    if queries.dtype != torch.bfloat16 or subkeys.dtype != torch.bfloat16:
+        raise ValueError("score_route_keys needs bf16 queries and sub-keys")
+    B, T, H, dk = queries.shape
+    L = subkeys.shape[1]
+    half = L // 2
+    if subkeys.ndim != 3 or subkeys.shape[0] != H or subkeys.shape[2] != dk or L % 2:
+        raise ValueError("score_route_keys needs sub-keys [H, 2*half, dk] matching the queries")
+    if not 1 <= width <= half * half:
+        raise ValueError("GL-SDM requires square slots and route sizes in [1, slots]")
+    shape = (B, T, H, width)
+    index = torch.empty(shape, dtype=torch.int64, device=device)
+    weights = torch.empty(shape, dtype=torch.float32, device=device)
+    addresses = torch.empty(shape, dtype=torch.int64, device=device)
+    keys = torch.empty(shape, dtype=torch.int64, device=device)
+    need = score_route_workspace_bytes(B, T, H, half, width) if split else 0
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    ws = workspace if need else None
+    N.call("glsdm_score_route_keys", N.ptr(queries), N.ptr(subkeys), B, T, H, dk, half, width, N.TIES[tie], offset,
+           chunk_size, num_layers, layer_idx, N.ptr(index), N.ptr(weights), N.ptr(addresses), N.ptr(keys),
+           N.ptr(ws), 0 if ws is None else ws.numel(), N.stream(device))
+    return index, weights, addresses, keys
+
+
 def absolute_addresses(values, index):
     """``(b*H + h)*S + index`` for ``index [B, T, H, width]``."""
     device = require_cuda(values, index)

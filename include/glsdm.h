@@ -139,6 +139,21 @@ int glsdm_score_route(const void *queries, const void *subkeys, int64_t B, int64
                       void *stream);
 
 /*
+ * Fused scoring + route that also emits the route's proposal addresses and
+ * collision keys: glsdm_score_route followed by glsdm_proposal_keys with the
+ * same (position_offset, chunk, layers, layer), in one launch.
+ *   addresses [B,T,H,width] int64 out: (b*H + h)*half*half + slot
+ *   keys      [B,T,H,width] int64 out: address*chunk*layers + (position_offset + t)*layers + layer
+ * Replaces: the write route of S/layers/global_layer.py:42-43 followed by the
+ * address/key construction of :45,52-53.
+ */
+int glsdm_score_route_keys(const void *queries, const void *subkeys, int64_t B, int64_t T, int64_t H,
+                           int32_t dk, int32_t half, int32_t width, int32_t tie, int64_t position_offset,
+                           int64_t chunk, int64_t layers, int64_t layer, int64_t *index, float *weights,
+                           int64_t *addresses, int64_t *keys, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
+/*
  * Workspace bytes glsdm_score_route can use for this shape (0: the shape
  * already fills the GPU and no workspace is used).  No counterpart in the
  * reference (which materialises the [B,T,H,2*half] scores instead).

@@ -78,3 +78,23 @@ def test_split_route_config3_epoch(device, tie):
     ridx, rw = c_oracle.route(scores.cpu(), 32, tie)
     assert torch.equal(idx.cpu(), ridx)
     torch.testing.assert_close(w.cpu(), rw, atol=2e-7, rtol=2e-6)
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("B,T,H,half,width,offset,chunk,layers,layer", [
+    (8, 512, 8, 256, 16, 0, 512, 1, 0), (2, 100, 3, 64, 8, 37, 512, 16, 6), (4, 512, 1, 1024, 32, 0, 512, 2, 1),
+    (1, 33, 2, 128, 64, 480, 512, 8, 7),
+])
+def test_score_route_keys_equals_route_then_keys(device, split, B, T, H, half, width, offset, chunk, layers, layer):
+    """glsdm_score_route_keys = glsdm_score_route + glsdm_proposal_keys, bit for bit
+    (both the single kernel and the split path)."""
+    q, k = _inputs(B, T, H, 128, half, seed=T + half + width)
+    qd, kd = q.to(device), k.to(device)
+    idx, w, addr, keys = hip.score_route_keys(qd, kd, width, offset, chunk, layers, layer, split=split)
+    ridx, rw, _ = hip.score_route(qd, kd, width, split=split)
+    assert torch.equal(idx, ridx) and torch.equal(w, rw)
+    bank = torch.empty(B, H, half * half, 1, device=device)
+    raddr, rkeys = hip.proposal_keys(bank, ridx, offset, chunk, layers, layer)
+    assert torch.equal(addr, raddr) and torch.equal(keys, rkeys)
+    pos = torch.arange(offset, offset + T, device=device).view(1, T, 1, 1)
+    assert torch.equal(keys, addr * (chunk * layers) + pos * layers + layer)
