@@ -145,6 +145,14 @@ __device__ __forceinline__ uint32_t key_index(double k, int tie)
     const uint32_t lo = (uint32_t)keyd_bits(k) & 0xFFFFu;
     return tie == GLSDM_TIE_HIGHEST ? lo : 0xFFFFu - lo;
 }
+// A 64-bit rank key of a factor element (index < 65536) as its double key
+// (the same order: the 16-bit tie bits are the low 16 of the 32-bit ones).
+__device__ __forceinline__ double narrow_keyd(uint64_t k)
+{
+    if (k == 0) return 0.0;
+    const uint64_t k48 = ((k >> 32) << 16) | (k & 0xFFFFu);
+    return __longlong_as_double((long long)((1ull << 52) + (k48 << 14)));
+}
 __device__ __forceinline__ uint64_t widen_key(double k, int tie)
 {
     return k != 0.0 ? rank_key(key_value(k), key_index(k, tie), tie) : 0;

@@ -470,21 +470,22 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
     const int kk = width < half ? width : half;
     const int npairs = staircase_build(s_pairs, kk, width);
     bool finite = true;
+    // the range lists hold 64-bit factor keys (index < 65536): merged as double keys
 #pragma unroll
     for (int f = 0; f < 2; ++f) {
-        uint64_t t[K];
+        double t[K];
         if (m < splits) {
             const uint64_t *src = parts + ((r * 2 + f) * splits + m) * K;
 #pragma unroll
-            for (int w = 0; w < K; ++w) t[w] = src[w];
+            for (int w = 0; w < K; ++w) t[w] = narrow_keyd(src[w]);
         } else {
             list_clear<K>(t);
         }
         for (int s = m + MG; s < splits; s += MG) {
             const uint64_t *src = parts + ((r * 2 + f) * splits + s) * K;
-            uint64_t c[K];
+            double c[K];
 #pragma unroll
-            for (int w = 0; w < K; ++w) c[w] = src[w];
+            for (int w = 0; w < K; ++w) c[w] = narrow_keyd(src[w]);
             merge_top<K>(t, c);
         }
         group_merge<K, MG>(t);
