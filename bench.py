@@ -492,6 +492,32 @@ def stack_model(cfg, dev):
     return model.eval()
 
 
+def full_stack_rate(dev, steps=2, warmup=1):
+    """Config 4's full-stack forward, reported beside the
+    headline memory-op line: tokens/s of Model.prefill on the whole batch."""
+    cfg = STACK_CONFIGS[4]
+    model = stack_model(cfg, dev)
+    inputs = torch.randint(cfg["vocab_size"], (cfg["B"], cfg["T"]), generator=torch.Generator("cpu").manual_seed(0))
+    inputs = inputs.to(dev)
+    for _ in range(warmup):
+        model.prefill(inputs)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        model.prefill(inputs)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del model
+    torch.cuda.empty_cache()
+    return {"value": round(cfg["B"] * cfg["T"] / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+            "steps": steps, "warmup": warmup,
+            "workload": "BASELINE configs[3]: 16-layer stack (8 local window-512 / 8 global, M=262144, k=16), "
+                        "d_model 1024, B=4, T=8192, bf16 random init; one step = Model.prefill of the batch "
+                        "(bench.py --config 4 reports it alone with its breakdown)"}
+
+
 def stack_main(args, dev):
     from glsdm.memory.backends import hip
     cfg = STACK_CONFIGS[args.config]
@@ -588,6 +614,8 @@ def main():
     ap.add_argument("--compare-schedules", action="store_true",
                     help="also time the other schedule (reported as ms_per_step_other_schedule)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-full-stack", action="store_true",
+                    help="skip the config-4 full-stack forward reported beside the headline line")
     ap.add_argument("--backward", action="store_true",
                     help="also run the read's backward every epoch: weights' and factor scores' gradients, and "
                          "the bank rows' gradient folded into the learned [H, S, D] bank (reported alongside; "
@@ -744,6 +772,9 @@ def main():
     }
     if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense":
         result["literal_scoring_mfma"] = literal_scoring(cfg, dev)
+    if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense" \
+            and not args.no_full_stack:
+        result["full_stack"] = full_stack_rate(dev)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
