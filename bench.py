@@ -492,6 +492,25 @@ def stack_model(cfg, dev):
     return model.eval()
 
 
+def device_copy_rate(dev, nbytes=1 << 30, reps=10):
+    """Bytes moved per second (read + write) by a 1 GiB device-to-device copy: the
+    practical streaming ceiling that the HBM roofline fractions are read against."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    rate = 2 * nbytes / (a.elapsed_time(b) / reps * 1e-3)
+    del src, dst
+    return rate
+
+
 def full_stack_rate(dev, steps=2, warmup=1):
     """Config 4's full-stack forward, reported beside the
     headline memory-op line: tokens/s of Model.prefill on the whole batch."""
@@ -714,7 +733,8 @@ def main():
     elif dominant == "commit":
         bytes_launch, t_launch = statistics.mean(commit_b), per_call["commit"] * 1e-3
         entry = "glsdm_commit_proposals" if args.write_path == "proposals" else "glsdm_commit"
-        roof = {"kernel": f"{entry} (pack + radix passes + segment)", "bound": "hbm", "unit": "GB/s",
+        roof = {"kernel": f"{entry} (prep + pack + top-digit pass + bucket sort + segment)", "bound": "hbm",
+                "unit": "GB/s",
                 "peak": HBM_PEAK / 1e9}
         achieved = bytes_launch / t_launch / 1e9
     else:
@@ -772,6 +792,13 @@ def main():
     }
     if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense":
         result["literal_scoring_mfma"] = literal_scoring(cfg, dev)
+    copy = device_copy_rate(dev)
+    result["hbm_calibration"] = {
+        "device_copy_GBps": round(copy / 1e9, 1), "copy_frac_of_peak": round(copy / HBM_PEAK, 4),
+        "roofline_achieved_frac_of_copy": round(roof["achieved"] * 1e9 / copy, 4),
+        "read_commit_frac_of_copy": round(alg_total / rc_time / copy, 4),
+        "note": "1 GiB device-to-device copy (read + write bytes / time): the streaming rate this MI355X "
+                "sustains; the fractions above are of the 8 TB/s nominal peak"}
     if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense" \
             and not args.no_full_stack:
         result["full_stack"] = full_stack_rate(dev)
