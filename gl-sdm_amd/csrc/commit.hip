@@ -74,7 +74,7 @@ struct CommitWorkspace {
     uint64_t *a, *b, *c;
     uint32_t *ghist;    // [MAX_PASSES][RADIX] global digit counts
     uint32_t *status;   // [passes][tiles][RADIX] look-back words
-    uint32_t *counter;  // [MAX_PASSES] tile-id counters, then one error word
+    uint32_t *counter;  // [MAX_PASSES] tile-id counters, an error word, the deferred-run count
     int64_t tiles;
     size_t status_words;
     size_t bytes;
@@ -88,7 +88,7 @@ static CommitWorkspace plan_workspace(void *base, int64_t entries, int passes)
     const size_t words = align256(sizeof(uint64_t) * (size_t)entries);
     const size_t ghist = align256(sizeof(uint32_t) * MAX_PASSES * RADIX);
     const size_t status = align256(sizeof(uint32_t) * w.status_words);
-    const size_t counter = align256(sizeof(uint32_t) * (MAX_PASSES + 1));
+    const size_t counter = align256(sizeof(uint32_t) * (MAX_PASSES + 2));
     char *p = static_cast<char *>(base);
     w.a = reinterpret_cast<uint64_t *>(p);
     w.b = reinterpret_cast<uint64_t *>(p + words);
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void commit_prep_kernel(uint32_t *__restrict__
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t i = tid; i < status_words; i += stride) status[i] = 0;
     if (tid < MAX_PASSES * RADIX) ghist[tid] = 0;
-    if (tid < MAX_PASSES + 1) counter[tid] = 0;
+    if (tid < MAX_PASSES + 2) counter[tid] = 0;
 }
 
 __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ addresses, int64_t rows,
@@ -563,12 +563,13 @@ template <typename TB> struct OverlayRows {
 // One wavefront per window of `win` (a power of two <= 64) consecutive sorted
 // positions; lane groups of `lpr` lanes (one bank row each) walk the address
 // runs that start in the window, continuing past its end when a run does.
-template <typename TB, typename SRC, typename ROWS, int VEC, int CH>
+template <typename TB, typename SRC, typename ROWS, int VEC, int CH, bool DEFER>
 __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t rows, int64_t D,
                                                       const int64_t *__restrict__ keys, const SRC src,
                                                       const uint64_t *__restrict__ sorted, int64_t n, int ebits,
                                                       int nv, int lpr, int win,
-                                                      unsigned long long *__restrict__ unique_out)
+                                                      unsigned long long *__restrict__ unique_out,
+                                                      int64_t *__restrict__ long_list, uint32_t *__restrict__ long_count)
 {
 #pragma clang fp contract(off)
     __shared__ uint64_t s_w[4][64];
@@ -594,6 +595,9 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
 
     const int ng = 64 / lpr;
     const int grp = lane / lpr, li = lane % lpr;
+    // whether the window's last run continues past it (wave-uniform)
+    bool crosses = false;
+    if constexpr (DEFER) crosses = p0 + win < n && (sorted[p0 + win] >> ebits) == (s_w[wave][win - 1] >> ebits);
     auto word_at = [&](int q) -> uint64_t { return q < win ? s_w[wave][q] : sorted[p0 + q]; };
     auto add_delta = [&](int64_t ent, const float (&old)[CH][VEC], float (&acc)[CH][VEC]) {
         if (ent >= n) return;                           // impossible after a correct sort; never read out of bounds
@@ -614,9 +618,19 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
         const uint64_t hw = s_w[wave][h];
         const int64_t row_addr = (int64_t)(hw >> ebits);
         if (row_addr >= rows) continue;                 // out-of-range entries: dropped
-        // run length: positions after the head with the same address
+        // run length: positions after the head with the same address.  DEFER
+        // (small windows, which long runs cross many of): a run that continues
+        // past the window is left to long_run_kernel
         int len = 1;
-        while (p0 + h + len < n && (int64_t)(word_at(h + len) >> ebits) == row_addr) ++len;
+        if constexpr (DEFER) {
+            while (h + len < win && p0 + h + len < n && (int64_t)(s_w[wave][h + len] >> ebits) == row_addr) ++len;
+            if (h + len == win && crosses) {
+                if (li == 0) long_list[atomicAdd(long_count, 1u)] = p0 + h;
+                continue;
+            }
+        } else {
+            while (p0 + h + len < n && (int64_t)(word_at(h + len) >> ebits) == row_addr) ++len;
+        }
         const TB *row = store.old_row(row_addr);
         float old[CH][VEC], acc[CH][VEC];
 #pragma unroll
@@ -679,10 +693,159 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
     }
 }
 
+// The runs segment_kernel left because they continue past their window (long
+// collision runs under skewed routes, or runs that straddle a window's end):
+// one lane group per run finds the run's end lpr positions at a time, fetches
+// lpr entry indices at a time, and sums the deltas in the same (key, entry)
+// order as segment_kernel, so the result is the same bit for bit.
+template <typename TB, typename SRC, typename ROWS, int VEC, int CH>
+__global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t D, const int64_t *__restrict__ keys,
+                                                       const SRC src, const uint64_t *__restrict__ sorted, int64_t n,
+                                                       int ebits, int nv, int lpr,
+                                                       const int64_t *__restrict__ long_list,
+                                                       const uint32_t *__restrict__ long_count)
+{
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int ng = 64 / lpr, grp = lane / lpr, li = lane % lpr;
+    const uint64_t mine = (lpr >= 64 ? ~0ull : ((1ull << lpr) - 1ull)) << (grp * lpr);
+    const uint64_t emask = (1ull << ebits) - 1ull;
+    const int64_t count = *long_count;
+    const int64_t groups = (int64_t)gridDim.x * 4 * ng;
+    auto key_of = [&](uint64_t word) -> int64_t {
+        const int64_t e = (int64_t)(word & emask);
+        return e < n ? keys[e] : INT64_MAX;
+    };
+    auto add_delta = [&](int64_t ent, const float (&old)[CH][VEC], float (&acc)[CH][VEC]) {
+        if (ent >= n) return;
+        const typename SRC::Entry e = src.entry(ent);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+            if (v < nv) {
+                float x[VEC];
+                src.template get<VEC>(e, v, old[c], x);
+#pragma unroll
+                for (int y = 0; y < VEC; ++y) acc[c][y] += x[y];
+            }
+        }
+    };
+    // every lane of a group runs the same iterations (group-uniform control flow)
+    for (int64_t i = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * ng + grp; i < count; i += groups) {
+        const int64_t hp = long_list[i];
+        const int64_t row_addr = (int64_t)(sorted[hp] >> ebits);
+        int len = 1;
+        for (;;) {
+            const int64_t at = hp + len + li;
+            const bool same = at < n && (int64_t)(sorted[at] >> ebits) == row_addr;
+            const uint64_t stop = __ballot(!same) & mine;
+            if (stop == 0) {
+                len += lpr;
+                continue;
+            }
+            len += __ffsll((unsigned long long)(stop >> (grp * lpr))) - 1;
+            break;
+        }
+        const TB *row = store.old_row(row_addr);
+        float old[CH][VEC], acc[CH][VEC];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+#pragma unroll
+            for (int x = 0; x < VEC; ++x) {
+                acc[c][x] = 0.0f;
+                old[c][x] = 0.0f;
+            }
+            if (v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
+        }
+        bool in_order = true;
+        if (keys) {
+            bool ok = true;
+            for (int q = 1 + li; q < len; q += lpr) ok &= key_of(sorted[hp + q]) >= key_of(sorted[hp + q - 1]);
+            in_order = (__ballot(!ok) & mine) == 0;
+        }
+        if (in_order) {
+            // PF entries' delta pieces are fetched before they are added (in order),
+            // so a long run is not one load latency per entry
+            constexpr int PF = CH * VEC >= 64 ? 1 : 64 / (CH * VEC);
+            for (int q0 = 0; q0 < len; q0 += lpr) {
+                const int q = q0 + li;
+                const int my_ent = q < len ? (int)(sorted[hp + q] & emask) : (int)n;
+                const int cnt = len - q0 < lpr ? len - q0 : lpr;
+                for (int j0 = 0; j0 < cnt; j0 += PF) {
+                    float x[PF][CH][VEC];
+                    bool have[PF];
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        const int j = j0 + u;
+                        const int ent = __shfl(my_ent, grp * lpr + (j < cnt ? j : 0));
+                        have[u] = j < cnt && ent < n;
+                        if (have[u]) {
+                            const typename SRC::Entry e = src.entry(ent);
+#pragma unroll
+                            for (int c = 0; c < CH; ++c) {
+                                const int v = li + c * lpr;
+                                if (v < nv) src.template get<VEC>(e, v, old[c], x[u][c]);
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < PF; ++u) {
+                        if (have[u]) {
+#pragma unroll
+                            for (int c = 0; c < CH; ++c) {
+                                const int v = li + c * lpr;
+                                if (v < nv) {
+#pragma unroll
+                                    for (int y = 0; y < VEC; ++y) acc[c][y] += x[u][c][y];
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        } else {
+            int64_t last_k = INT64_MIN, last_e = -1;
+            for (int r2 = 0; r2 < len; ++r2) {
+                int64_t best_k = INT64_MAX, best_e = INT64_MAX;
+                for (int q = 0; q < len; ++q) {
+                    const uint64_t wq = sorted[hp + q];
+                    const int64_t e = (int64_t)(wq & emask);
+                    const int64_t k = key_of(wq);
+                    const bool after = k > last_k || (k == last_k && e > last_e);
+                    const bool before = k < best_k || (k == best_k && e < best_e);
+                    if (after && before) { best_k = k; best_e = e; }
+                }
+                add_delta(best_e, old, acc);
+                last_k = best_k;
+                last_e = best_e;
+            }
+        }
+        TB *dst = store.new_row(row_addr, li, hp);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int v = li + c * lpr;
+            if (v < nv) {
+#pragma unroll
+                for (int x = 0; x < VEC; ++x) old[c][x] = old[c][x] + acc[c][x];
+                VecStore<TB, VEC>::store(dst + (int64_t)v * VEC, old[c]);
+            }
+        }
+    }
+}
+
+// Where segment_kernel leaves the runs that continue past their window: a
+// word buffer of the workspace that the sorted words are not in, and a
+// counter that commit_prep_kernel zeroed.
+struct LongRuns {
+    int64_t *list;
+    uint32_t *count;
+};
+
 template <typename TB, int VEC, typename SRC, typename ROWS>
 static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                              const uint64_t *sorted, int64_t n, int ebits, const RowPlan &p,
-                             int64_t *unique_out, hipStream_t st)
+                             int64_t *unique_out, const LongRuns &lr, hipStream_t st)
 {
     // window: 64 positions per wave when that still makes GLSDM_SEG_WAVES waves,
     // shorter for small commits (so they fill the chip), never below one
@@ -692,9 +855,26 @@ static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const i
     while (win > groups && ceil_div(n, win) < GLSDM_SEG_WAVES) win >>= 1;
     const dim3 grid((unsigned)ceil_div(n, 4 * win)), block(256);
     auto *u = reinterpret_cast<unsigned long long *>(unique_out);
+    // mid-sized windows (commits of a few 10^4 entries, where skewed runs cross many
+    // windows): runs that cross a window go to long_run_kernel, at most one per
+    // window.  Full windows see few, short crossings; in tiny windows (tiny
+    // commits) nearly every repeated address crosses, and the second launch costs
+    // more than it saves (measured)
+    const bool defer = win >= 8 && win < 64;
+    const int64_t windows = ceil_div(n, win);
+    const dim3 lgrid((unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(windows, 4 * groups), 4096)));
 #define GLSDM_SEG_LAUNCH(C)                                                                                 \
-    hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C>), grid, block, 0, st, store, rows, D, keys, src, \
-                       sorted, n, ebits, p.nv, p.lpr, win, u)
+    if (defer) {                                                                                              \
+        hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C, true>), grid, block, 0, st, store, rows, D,  \
+                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, lr.list, lr.count);              \
+        if ((rc = check_launch("segment_kernel"))) return rc;                                                 \
+        hipLaunchKernelGGL((long_run_kernel<TB, SRC, ROWS, VEC, C>), lgrid, block, 0, st, store, D, keys, src, \
+                           sorted, n, ebits, p.nv, p.lpr, lr.list, lr.count);                                 \
+    } else {                                                                                                  \
+        hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C, false>), grid, block, 0, st, store, rows, D, \
+                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, nullptr, nullptr);               \
+    }
+    int rc;
     switch (p.ch) {
     case 1: GLSDM_SEG_LAUNCH(1); break;
     case 2: GLSDM_SEG_LAUNCH(2); break;
@@ -703,7 +883,7 @@ static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const i
     default: GLSDM_SEG_LAUNCH(8); break;
     }
 #undef GLSDM_SEG_LAUNCH
-    return check_launch("segment_kernel");
+    return check_launch("long_run_kernel");
 }
 
 // One vector width for bank and delta rows: the wider element type's 16-byte
@@ -711,7 +891,7 @@ static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const i
 template <typename TB, typename TD, typename SRC, typename ROWS>
 static int launch_segment_rows(const ROWS &store, uintptr_t row_bits, int64_t rows, int64_t D, const int64_t *keys,
                                const SRC &src, const void *delta_rows, const uint64_t *sorted, int64_t n,
-                               int ebits, int64_t *unique_out, hipStream_t st)
+                               int ebits, int64_t *unique_out, const LongRuns &lr, hipStream_t st)
 {
     constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
     const bool aligned = ((row_bits | reinterpret_cast<uintptr_t>(delta_rows)) & 15) == 0;
@@ -719,20 +899,20 @@ static int launch_segment_rows(const ROWS &store, uintptr_t row_bits, int64_t ro
         RowPlan p{VEC, (int)(D / VEC), 0, 0};
         p.lpr = pow2_ceil(p.nv) < 64 ? pow2_ceil(p.nv) : 64;
         p.ch = (int)ceil_div(p.nv, p.lpr);
-        return launch_segment_ch<TB, VEC>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
+        return launch_segment_ch<TB, VEC>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, lr, st);
     }
     RowPlan p{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
-    return launch_segment_ch<TB, 1>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, st);
+    return launch_segment_ch<TB, 1>(store, rows, D, keys, src, sorted, n, ebits, p, unique_out, lr, st);
 }
 
 // The bank itself as the row store.
 template <typename TB, typename TD, typename SRC>
 static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                             const void *delta_rows, const uint64_t *sorted, int64_t n, int ebits,
-                            int64_t *unique_out, hipStream_t st)
+                            int64_t *unique_out, const LongRuns &lr, hipStream_t st)
 {
     return launch_segment_rows<TB, TD>(DenseRows<TB>{static_cast<TB *>(bank), D}, reinterpret_cast<uintptr_t>(bank),
-                                       rows, D, keys, src, delta_rows, sorted, n, ebits, unique_out, st);
+                                       rows, D, keys, src, delta_rows, sorted, n, ebits, unique_out, lr, st);
 }
 
 }  // namespace glsdm
@@ -772,10 +952,11 @@ static int check_commit(const char *what, int64_t rows, int64_t D, int64_t entri
 }
 
 // Steps 1-3 of the pipeline: the packed (address, entry) words sorted by
-// address, in *sorted (one of the two workspace word buffers).
+// address, in *sorted (one of the workspace word buffers); *long_runs is
+// another, free one, for the segment step's deferred runs.
 static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
                        size_t workspace_bytes, const char *what, const uint64_t **sorted, int *ebits_out,
-                       hipStream_t st)
+                       LongRuns *long_runs, hipStream_t st)
 {
     const int ebits = entry_bits(entries), abits = address_bits(rows);
     const int passes = pass_count(abits);
@@ -804,6 +985,7 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
         *sorted = ws.c;
         *ebits_out = ebits;
+        *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.a), ws.counter + MAX_PASSES + 1};
         return GLSDM_OK;
     }
 #endif
@@ -821,15 +1003,18 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
     }
     *sorted = src;
     *ebits_out = ebits;
+    // the sorted words are in a or b; c is free for the deferred runs
+    *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.c), ws.counter + MAX_PASSES + 1};
     return GLSDM_OK;
 }
 
 template <typename TB, typename TD>
 static int segment_stored(void *bank, int64_t rows, int64_t D, const int64_t *keys, const void *deltas,
-                          const uint64_t *sorted, int64_t n, int ebits, int64_t *unique_out, hipStream_t st)
+                          const uint64_t *sorted, int64_t n, int ebits, int64_t *unique_out, const LongRuns &lr,
+                          hipStream_t st)
 {
     const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};
-    return launch_segment_t<TB, TD>(bank, rows, D, keys, src, deltas, sorted, n, ebits, unique_out, st);
+    return launch_segment_t<TB, TD>(bank, rows, D, keys, src, deltas, sorted, n, ebits, unique_out, lr, st);
 }
 
 extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
@@ -846,15 +1031,16 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit", &sorted, &ebits, st)))
+    LongRuns lr{nullptr, nullptr};
+    if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit", &sorted, &ebits, &lr, st)))
         return rc;
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
-        return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
+        return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
-        return segment_stored<float, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
+        return segment_stored<float, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
     if (bank_dtype == GLSDM_BF16 && delta_dtype == GLSDM_F32)
-        return segment_stored<bf16_t, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
-    return segment_stored<bf16_t, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, st);
+        return segment_stored<bf16_t, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
+    return segment_stored<bf16_t, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
 }
 
 extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
@@ -878,15 +1064,16 @@ extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t ro
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
+    LongRuns lr{nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit_proposals", &sorted,
-                          &ebits, st)))
+                          &ebits, &lr, st)))
         return rc;
     const ProposalTerms src{error, decay, weights, mass, D, (uint32_t)width, (uint32_t)heads};
     if (bank_dtype == GLSDM_F32)
         return launch_segment_t<float, float>(bank, rows, D, keys, src, error, sorted, entries, ebits,
-                                              unique_out, st);
+                                              unique_out, lr, st);
     return launch_segment_t<bf16_t, float>(bank, rows, D, keys, src, error, sorted, entries, ebits, unique_out,
-                                           st);
+                                           lr, st);
 }
 
 extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t D, const int64_t *addresses,
@@ -907,12 +1094,13 @@ extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t 
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
+    LongRuns lr{nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "read_backward_rows", &sorted,
-                          &ebits, st)))
+                          &ebits, &lr, st)))
         return rc;
     const ReadGradTerms src{weights, grad_out, D, (uint32_t)width};
     return launch_segment_t<float, float>(grad_bank, rows, D, nullptr, src, grad_out, sorted, entries, ebits,
-                                          nullptr, st);
+                                          nullptr, lr, st);
 }
 
 extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, int64_t S, int64_t D,
@@ -936,8 +1124,9 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
+    LongRuns lr{nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "overlay_commit", &sorted, &ebits,
-                          st)))
+                          &lr, st)))
         return rc;
     const uintptr_t row_bits = reinterpret_cast<uintptr_t>(base) | reinterpret_cast<uintptr_t>(pool);
 #define GLSDM_OVERLAY(TB, TD)                                                                                  \
@@ -946,7 +1135,7 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
                                  pool_offset};                                                                \
         const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};                                       \
         return launch_segment_rows<TB, TD>(ov, row_bits, rows, D, keys, src, deltas, sorted, entries, ebits,  \
-                                           unique_out, st);                                                   \
+                                           unique_out, lr, st);                                               \
     }
     if (dtype == GLSDM_F32 && delta_dtype == GLSDM_F32) GLSDM_OVERLAY(float, float)
     if (dtype == GLSDM_F32) GLSDM_OVERLAY(float, bf16_t)

@@ -147,3 +147,55 @@ def test_commit_bucket_sort_paths(device, keyed, rows, D, E, lo, hi):
     keep = addr < rows                                      # the oracle takes in-range entries only
     ref, _ = c_oracle.commit(flat, addr[keep], delta[keep], None if keys is None else keys[keep])
     assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("E", [70_000, 100_000, 200_000])
+def test_commit_long_runs_past_windows(device, dtype, E):
+    """Commits of ~1e5 entries use windows of 8-32 sorted positions per wave, so
+    runs that continue past their window go to the long-run kernel: hot
+    addresses with thousands of entries (keys in arrival order), warm ones whose
+    keys run against arrival order (the selection path), and out-of-range
+    entries.  Bitwise equal to the oracle's sequential per-address sums."""
+    g = torch.Generator().manual_seed(E)
+    rows, D = 4096, 64
+    addr = torch.randint(0, rows, (E,), generator=g)
+    pick = torch.rand(E, generator=g)
+    hot = torch.randint(0, rows, (16,), generator=g)
+    warm = torch.randint(0, rows, (64,), generator=g)
+    h = pick < 0.5
+    addr[h] = hot[torch.randint(0, 16, (int(h.sum()),), generator=g)]
+    w = (pick >= 0.5) & (pick < 0.52)
+    addr[w] = warm[torch.randint(0, 64, (int(w.sum()),), generator=g)]
+    addr[::997] = rows + 3                                   # out of range: dropped
+    ent = torch.arange(E)
+    keys = addr * (E + 1) + ent
+    rev = torch.isin(addr, warm)
+    keys[rev] = addr[rev] * (E + 1) + (E - ent[rev])
+    flat = torch.randn(rows, D, generator=g).to(dtype)
+    delta = torch.randn(E, D, generator=g) * 0.02
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
+    keep = addr < rows
+    if dtype == torch.float32:
+        ref = torch_oracle.commit(flat, addr[keep], delta[keep], keys[keep])
+    else:
+        ref = torch_oracle.commit_bf16(flat, addr[keep], delta[keep], keys[keep])
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_overlay_commit_long_runs_equal_dense(device):
+    """The overlay row store through the long-run kernel: same bits as the dense bank."""
+    from glsdm.memory import OverlayView
+    g = torch.Generator().manual_seed(5)
+    B, H, S, D, E = 2, 2, 1024, 32, 90_000
+    base = torch.randn(H, S, D, generator=g)
+    rows = B * H * S
+    addr = torch.randint(0, rows, (E,), generator=g)
+    addr[: E // 2] = torch.randint(0, 8, (E // 2,), generator=g) * 97     # 8 hot rows, long runs
+    keys = addr * (E + 1) + torch.arange(E)
+    delta = torch.randn(E, D, generator=g) * 0.02
+    ov = OverlayView.from_base(base.to(device), B)
+    ov.commit(addr.to(device), delta.to(device), keys.to(device))
+    dense = base.unsqueeze(0).expand(B, -1, -1, -1).reshape(rows, D).clone()
+    ref = torch_oracle.commit(dense, addr, delta, keys)
+    assert torch.equal(ov.materialise().cpu().reshape(rows, D), ref)
