@@ -954,6 +954,23 @@ static int check_commit(const char *what, int64_t rows, int64_t D, int64_t entri
 // Steps 1-3 of the pipeline: the packed (address, entry) words sorted by
 // address, in *sorted (one of the workspace word buffers); *long_runs is
 // another, free one, for the segment step's deferred runs.
+// Where commit_sort leaves the sorted words and the deferred-run list for
+// (rows, entries): a function of the shape alone, so a later call (the apply
+// step) finds them without state.
+static void sort_result(const CommitWorkspace &ws, int passes, const uint64_t **sorted, LongRuns *long_runs)
+{
+#if GLSDM_BUCKET_SORT
+    if (passes >= 3) {
+        *sorted = ws.c;
+        *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.a), ws.counter + MAX_PASSES + 1};
+        return;
+    }
+#endif
+    // LSD passes ping-pong a -> b -> a ...; c is free for the deferred runs
+    *sorted = passes % 2 == 0 ? ws.a : ws.b;
+    *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.c), ws.counter + MAX_PASSES + 1};
+}
+
 static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
                        size_t workspace_bytes, const char *what, const uint64_t **sorted, int *ebits_out,
                        LongRuns *long_runs, hipStream_t st)
@@ -983,9 +1000,8 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
         hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.a, ws.c, ws.ghist,
                            ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
-        *sorted = ws.c;
+        sort_result(ws, passes, sorted, long_runs);
         *ebits_out = ebits;
-        *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.a), ws.counter + MAX_PASSES + 1};
         return GLSDM_OK;
     }
 #endif
@@ -1001,10 +1017,9 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
         if ((rc = check_launch("onesweep_kernel"))) return rc;
         uint64_t *t = src; src = dst; dst = t;
     }
-    *sorted = src;
+    sort_result(ws, passes, sorted, long_runs);
+    if (*sorted != src) return fail(GLSDM_ERR_ARG, "%s: internal sort buffer mismatch", what);
     *ebits_out = ebits;
-    // the sorted words are in a or b; c is free for the deferred runs
-    *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.c), ws.counter + MAX_PASSES + 1};
     return GLSDM_OK;
 }
 
@@ -1015,6 +1030,19 @@ static int segment_stored(void *bank, int64_t rows, int64_t D, const int64_t *ke
 {
     const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};
     return launch_segment_t<TB, TD>(bank, rows, D, keys, src, deltas, sorted, n, ebits, unique_out, lr, st);
+}
+
+static int commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, const void *deltas,
+                        int32_t delta_dtype, const int64_t *keys, int64_t entries, const uint64_t *sorted, int ebits,
+                        int64_t *unique_out, const LongRuns &lr, hipStream_t st)
+{
+    if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
+        return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
+    if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
+        return segment_stored<float, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
+    if (bank_dtype == GLSDM_BF16 && delta_dtype == GLSDM_F32)
+        return segment_stored<bf16_t, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
+    return segment_stored<bf16_t, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
 }
 
 extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
@@ -1034,13 +1062,45 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
     LongRuns lr{nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit", &sorted, &ebits, &lr, st)))
         return rc;
-    if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
-        return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
-    if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_BF16)
-        return segment_stored<float, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
-    if (bank_dtype == GLSDM_BF16 && delta_dtype == GLSDM_F32)
-        return segment_stored<bf16_t, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
-    return segment_stored<bf16_t, bf16_t>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
+    return commit_apply(bank, bank_dtype, rows, D, deltas, delta_dtype, keys, entries, sorted, ebits, unique_out,
+                        lr, st);
+}
+
+extern "C" int glsdm_commit_prepare(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
+                                    size_t workspace_bytes, void *stream)
+{
+    if (rows < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit_prepare: bad shape");
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("commit_prepare", rows, 1, entries);
+    if (rc) return rc;
+    if (!addresses) return fail(GLSDM_ERR_ARG, "commit_prepare: null pointer");
+    const uint64_t *sorted = nullptr;
+    int ebits = 0;
+    LongRuns lr{nullptr, nullptr};
+    return commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit_prepare", &sorted, &ebits, &lr,
+                       as_stream(stream));
+}
+
+extern "C" int glsdm_commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, const void *deltas,
+                                  int32_t delta_dtype, const int64_t *keys, int64_t entries, void *workspace,
+                                  size_t workspace_bytes, int64_t *unique_out, void *stream)
+{
+    if (rows < 1 || D < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit_apply: bad shape");
+    if (!dtype_ok(bank_dtype) || !dtype_ok(delta_dtype)) return fail(GLSDM_ERR_ARG, "commit_apply: bad dtype");
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("commit_apply", rows, D, entries);
+    if (rc) return rc;
+    if (!bank || !deltas) return fail(GLSDM_ERR_ARG, "commit_apply: null pointer");
+    const int passes = pass_count(address_bits(rows));
+    const CommitWorkspace ws = plan_workspace(workspace, entries, passes);
+    if (!workspace || workspace_bytes < ws.bytes)
+        return fail(GLSDM_ERR_WORKSPACE, "commit_apply: workspace of %zu bytes needed, %zu given", ws.bytes,
+                    workspace_bytes);
+    const uint64_t *sorted = nullptr;
+    LongRuns lr{nullptr, nullptr};
+    sort_result(ws, passes, &sorted, &lr);
+    return commit_apply(bank, bank_dtype, rows, D, deltas, delta_dtype, keys, entries, sorted, entry_bits(entries),
+                        unique_out, lr, as_stream(stream));
 }
 
 extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,

@@ -34,6 +34,8 @@ SIGNATURES = {
     "glsdm_score_route_workspace_bytes": ([_I64, _I64, _I64, _I32, _I32, ctypes.POINTER(_SZ)], _I32),
     "glsdm_commit_workspace_bytes": ([_I64, _I64, ctypes.POINTER(_SZ)], _I32),
     "glsdm_commit": ([_P, _I32, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),
+    "glsdm_commit_prepare": ([_I64, _P, _I64, _P, _SZ, _P], _I32),
+    "glsdm_commit_apply": ([_P, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),
     "glsdm_absolute_addresses": ([_P, _I64, _I64, _I64, _I32, _I64, _P, _P], _I32),
     "glsdm_proposal_keys": ([_P, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),
     "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),

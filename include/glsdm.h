@@ -193,6 +193,25 @@ int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
                  int64_t *unique_out, void *stream);
 
 /*
+ * glsdm_commit in two steps: glsdm_commit_prepare groups the entries by address
+ * (the sort; it reads only the addresses, never the bank) into the workspace,
+ * and glsdm_commit_apply, later on any stream ordered after it, runs the
+ * segmented sums and the read-modify-write of the touched rows from that
+ * workspace.  The pair with the same (rows, entries, workspace) equals
+ * glsdm_commit bit for bit; the workspace must not be reused in between.  A
+ * pipelined caller can sort epoch e+1's entries while epoch e's commit updates
+ * the bank (the sort does not depend on the bank).
+ * Replaces: the stable key sort + unique_consecutive of
+ * S/memory/transactions.py:89-91 (prepare) and the segment_reduce + index_copy
+ * of :92-96 (apply).
+ */
+int glsdm_commit_prepare(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
+                         size_t workspace_bytes, void *stream);
+int glsdm_commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, const void *deltas,
+                       int32_t delta_dtype, const int64_t *keys, int64_t entries, void *workspace,
+                       size_t workspace_bytes, int64_t *unique_out, void *stream);
+
+/*
  * Absolute addresses (b*H + h)*S + index[b,t,h,j] for index [B,T,H,width].
  * Replaces: S/memory/routing.py:31-34 (absolute_addresses) and
  * S/memory/transactions.py:13-16 (addresses, with requests = arange(B)).

@@ -199,3 +199,34 @@ def test_overlay_commit_long_runs_equal_dense(device):
     dense = base.unsqueeze(0).expand(B, -1, -1, -1).reshape(rows, D).clone()
     ref = torch_oracle.commit(dense, addr, delta, keys)
     assert torch.equal(ov.materialise().cpu().reshape(rows, D), ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,D,E", [(5000, 32, 3000), (1 << 22, 128, 60_000), (70_000, 16, 100_000),
+                                      (1 << 20, 64, 250_000)])
+def test_commit_prepare_apply_equals_commit(device, dtype, rows, D, E):
+    """glsdm_commit_prepare then glsdm_commit_apply (here with other work and
+    another epoch's prepare in between, on another stream) equals glsdm_commit
+    bit for bit, on the LSD path (few address digits) and the top-digit + bucket
+    path, with keys."""
+    from glsdm import _native as N
+    g = torch.Generator().manual_seed(rows + E)
+    flat = (torch.randn(rows, D, generator=g)).to(dtype)
+    addr = torch.randint(0, rows, (E,), generator=g)
+    addr[: E // 10] = addr[E // 10: 2 * (E // 10)]                    # collisions
+    delta = (torch.randn(E, D, generator=g) * 0.02).to(dtype)
+    keys = addr * (E + 1) + torch.randperm(E, generator=g)
+    ref = hip.commit(flat.to(device), addr.to(device), delta.to(device), keys.to(device))
+    need = hip.commit_workspace_bytes(E, rows)
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    ws2 = torch.empty(need, dtype=torch.uint8, device=device)
+    bank, a, d, k = flat.to(device), addr.to(device), delta.to(device), keys.to(device)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        N.call("glsdm_commit_prepare", rows, N.ptr(a), E, N.ptr(ws), need, N.stream(device))
+        N.call("glsdm_commit_prepare", rows, N.ptr(a.flip(0).contiguous()), E, N.ptr(ws2), need, N.stream(device))
+    torch.cuda.current_stream(device).wait_stream(side)
+    N.call("glsdm_commit_apply", N.ptr(bank), N.dtype_code(bank), rows, D, N.ptr(d), N.dtype_code(d), N.ptr(k), E,
+           N.ptr(ws), need, None, N.stream(device))
+    assert torch.equal(bank, ref)
