@@ -20,6 +20,11 @@
 //                 earlier tiles' published counts.  The entry bits below ebits
 //                 are never sorted: they start ascending and every pass is
 //                 stable, so each address's entries end up in arrival order.
+//      Addresses of three or more digits (2^16 rows or more) take the bucket path
+//      instead of steps 1-3, two launches: each tile packs its words and orders
+//      them stably by the top address digit in LDS, recording where each
+//      digit's piece lies; then a block per top digit gathers its pieces from
+//      every tile, in tile order, and sorts them by the remaining digits.
 //   4. segment:   a wavefront per 64 sorted positions reads the addresses from
 //                 the sorted words, finds run heads with a ballot, and its lane
 //                 groups each walk one run, summing the deltas in fp32 registers
@@ -41,7 +46,7 @@ namespace glsdm {
 constexpr int RADIX_BITS = 8;
 constexpr int RADIX = 1 << RADIX_BITS;
 #ifndef GLSDM_BUCKET_SORT
-#define GLSDM_BUCKET_SORT 1                              // top-digit pass + per-bucket LDS sort
+#define GLSDM_BUCKET_SORT 1                              // tile-local top digit + per-bucket sort
 #endif
 #ifndef GLSDM_SORT_THREADS
 #define GLSDM_SORT_THREADS 512
@@ -275,13 +280,13 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
     }
 }
 
-// Second step of the address sort when the address needs three or more 8-bit
-// digits: one onesweep pass has grouped the words by their top address digit
-// (256 buckets, stable), and one block per bucket sorts its words by the
+// The address sort when the address needs three or more 8-bit digits (the
+// bucket path, two launches): the words are grouped by their top address digit
+// (256 buckets, stable) and one block per bucket sorts its words by the
 // remaining address digits, least significant first, each pass stable, so the
-// result equals the full LSD sort.  A bucket of up to BK_CAP words is loaded
-// into LDS once and sorted there; a larger one (skewed addresses) is sorted
-// in chunks of BK_CAP through global scratch, with a counting pass per digit.
+// result equals the full LSD sort.  A bucket of up to BK_CAP words is sorted
+// in LDS; a larger one (skewed addresses) in chunks of BK_CAP through global
+// scratch, with a counting pass per digit.
 constexpr int BK_THREADS = 1024;
 constexpr int BK_ITEMS = 8;
 constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // 8192 words
@@ -332,40 +337,192 @@ __device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const boo
     __syncthreads();                                      // the wave prefixes are read by every thread
 }
 
-__global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__restrict__ in,
-                                                                 uint64_t *__restrict__ scratch,
-                                                                 uint64_t *__restrict__ out,
-                                                                 const uint32_t *__restrict__ ghist, int ebits,
-                                                                 int lpasses)
+// Bucket path, step 1: each tile of SORT_TILE consecutive entries packs its words, orders them stably by the top
+// address digit in LDS and stores them in that order at the tile's own
+// position, with one word per (digit, tile) -- the tile's first position of
+// the digit << 16 | the digit's count in the tile -- stored digit-major, so the
+// block that sorts a bucket reads its pieces of every tile in one coalesced
+// load.  Block 0 also clears the workspace's counter words.
+static_assert(SORT_TILE < 65536, "tile positions and counts are 16-bit");
+
+__global__ __launch_bounds__(SORT_THREADS) void tile_bucket_kernel(const int64_t *__restrict__ addresses,
+                                                                   int64_t rows, int ebits, int shift, int64_t n,
+                                                                   uint64_t *__restrict__ out,
+                                                                   uint32_t *__restrict__ pieces, int64_t tiles,
+                                                                   uint32_t *__restrict__ counter)
+{
+    __shared__ uint32_t cnt[SORT_WAVES][RADIX];
+    __shared__ uint32_t s_wsum[RADIX / 64];
+    __shared__ uint32_t lstart[RADIX];
+    __shared__ uint64_t s_items[SORT_TILE];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const bool owner = tid < RADIX;
+    const int64_t tile = blockIdx.x;
+    if (tile == 0 && tid < MAX_PASSES + 2) counter[tid] = 0;
+    for (int x = tid; x < SORT_WAVES * RADIX; x += SORT_THREADS) (&cnt[0][0])[x] = 0;
+    __syncthreads();
+
+    // stable rank of each item among its wave's items of the same digit
+    const uint64_t lt = (1ull << lane) - 1ull;
+    const int64_t start = tile * SORT_TILE + (int64_t)wave * WAVE_ITEMS;
+    uint64_t v[SORT_ITEMS];
+    uint32_t dig[SORT_ITEMS], pos[SORT_ITEMS];
+#pragma unroll
+    for (int k = 0; k < SORT_ITEMS; ++k) {
+        const int64_t i = start + k * 64 + lane;
+        const bool valid = i < n;
+        const int64_t a = valid ? addresses[i] : 0;
+        const uint64_t row = (a >= 0 && a < rows) ? (uint64_t)a : (uint64_t)rows;   // out of range: one run, dropped
+        v[k] = (row << ebits) | (uint64_t)i;
+        const uint32_t d = (uint32_t)(v[k] >> shift) & (RADIX - 1);
+        dig[k] = d;
+        uint64_t peers = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < RADIX_BITS; ++bit) {
+            const bool on = (d >> bit) & 1u;
+            const uint64_t m = __ballot(on);
+            peers &= on ? m : ~m;
+        }
+        const uint32_t before = (uint32_t)__popcll(peers & lt);
+        uint32_t c = 0;
+        if (valid) c = cnt[wave][d];
+        pos[k] = c + before;
+        if (valid && before == 0) cnt[wave][d] = c + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+
+    // digit owners: per-wave prefixes and the tile's count of their digit
+    uint32_t total = 0;
+    if (owner) {
+#pragma unroll
+        for (int w = 0; w < SORT_WAVES; ++w) {
+            const uint32_t x = cnt[w][tid];
+            cnt[w][tid] = total;
+            total += x;
+        }
+    }
+    const uint32_t first = digit_scan(total, s_wsum) - total;    // its barrier publishes the wave prefixes
+    if (owner) {
+        lstart[tid] = first;
+        pieces[(int64_t)tid * tiles + tile] = first << 16 | total;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SORT_ITEMS; ++k) {
+        const int64_t i = start + k * 64 + lane;
+        const uint32_t at = lstart[dig[k]] + cnt[wave][dig[k]] + pos[k];
+        if (i < n && at < (uint32_t)SORT_TILE) s_items[at] = v[k];
+    }
+    __syncthreads();
+    const int64_t tile_n = n - tile * SORT_TILE;
+    const int valid_items = tile_n < SORT_TILE ? (int)tile_n : SORT_TILE;
+#pragma unroll
+    for (int k = 0; k < SORT_ITEMS; ++k) {
+        const int j = k * SORT_THREADS + tid;
+        if (j < valid_items) out[tile * SORT_TILE + j] = s_items[j];
+    }
+}
+
+// Inclusive prefix sum over the BK_THREADS threads of a block (every thread
+// calls it); *total gets the block's sum.
+__device__ __forceinline__ uint32_t block_scan(uint32_t x, uint32_t *s_w, uint32_t *total)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) s_w[wave] = x;
+    __syncthreads();
+    uint32_t add = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < BK_WAVES; ++w) {
+        const uint32_t y = s_w[w];
+        add += w < wave ? y : 0u;
+        sum += y;
+    }
+    __syncthreads();                                      // s_w is free again
+    *total = sum;
+    return x + add;
+}
+
+// Bucket path, step 2: one block per top digit gathers its pieces in tile
+// order (tiles hold increasing entry ranges, so the gathered bucket is in entry
+// order within each address) and sorts them by the remaining address digits,
+// in LDS up to BK_CAP words, else in global memory; the words of bucket d end
+// at positions [start_d, start_d + size_d) of out, start_d the count of words
+// with a smaller top digit.
+__global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(const uint64_t *__restrict__ in,
+                                                                      const uint32_t *__restrict__ pieces,
+                                                                      int64_t tiles, int64_t n,
+                                                                      uint64_t *__restrict__ scratch,
+                                                                      uint64_t *__restrict__ out, int ebits,
+                                                                      int lpasses)
 {
     __shared__ uint64_t s_x[BK_CAP];
     __shared__ uint64_t s_y[BK_CAP];
     __shared__ uint32_t cnt[BK_WAVES][RADIX];
     __shared__ uint32_t lstart[RADIX];
     __shared__ uint32_t s_wsum[2][RADIX / 64];
+    __shared__ uint32_t s_scan[BK_WAVES];
     __shared__ int64_t s_base[RADIX];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int bucket = blockIdx.x;
-    // the bucket's range: exclusive prefix of the top-digit histogram
-    const uint32_t own = tid < RADIX ? ghist[tid] : 0u;
-    const uint32_t excl = digit_scan(own, s_wsum[0]) - own;
-    if (tid == bucket) lstart[0] = excl;
-    __syncthreads();
-    const int64_t start = lstart[0];
-    const int64_t size = ghist[bucket];
-    if (size == 0) return;                                  // block-uniform
-    if (size <= BK_CAP) {
-        // wi item slots per thread: each wave takes wi*64 consecutive words, so all
-        // waves share the work and (wave, slot, lane) is still position order
+    const uint32_t *mine = pieces + (int64_t)blockIdx.x * tiles;
+    // the bucket's size and start: sums over the tiles of its piece counts and first positions
+    uint32_t my_cnt = 0, my_first = 0;
+    for (int64_t t = tid; t < tiles; t += BK_THREADS) {
+        const uint32_t w = mine[t];
+        my_cnt += w & 0xffffu;
+        my_first += w >> 16;
+    }
+    uint32_t size32, start32;
+    block_scan(my_cnt, s_scan, &size32);
+    block_scan(my_first, s_scan, &start32);
+    const int64_t size = size32, start = start32;
+    if (size == 0 || start + size > n) return;              // block-uniform; the second never holds
+    const bool in_lds = size <= BK_CAP;
+    // global path: gather into X, then passes X -> Y -> X ..., the last one into out
+    uint64_t *X = ((lpasses % 2 == 0) ? out : scratch) + start;
+    uint64_t *Y = ((lpasses % 2 == 0) ? scratch : out) + start;
+    // up to BK_THREADS tiles at a time: the pieces' inclusive prefix and source
+    // positions in LDS (in cnt, which the ranking clears before use), then every
+    // thread copies words j, j + BK_THREADS, ..., finding each one's tile by
+    // binary search, so consecutive threads copy consecutive words
+    static_assert(2 * BK_THREADS <= BK_WAVES * RADIX, "gather tables fit in cnt");
+    uint32_t *s_pref = &cnt[0][0], *s_from = &cnt[0][0] + BK_THREADS;
+    uint32_t carry = 0;
+    for (int64_t c0 = 0; c0 < tiles; c0 += BK_THREADS) {   // block-uniform trip count
+        const int64_t t = c0 + tid;
+        const uint32_t w = t < tiles ? mine[t] : 0u;
+        uint32_t chunk;
+        const uint32_t incl = block_scan(w & 0xffffu, s_scan, &chunk);   // its barriers end the last round's reads
+        s_pref[tid] = incl;
+        s_from[tid] = (uint32_t)(t * SORT_TILE + (w >> 16));            // < n <= 2^30
+        __syncthreads();
+        const int last = (int)(tiles - c0 < BK_THREADS ? tiles - c0 : BK_THREADS) - 1;
+        for (uint32_t j = tid; j < chunk; j += BK_THREADS) {
+            int lo = 0, hi = last;                                     // first tile whose prefix exceeds j
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (s_pref[mid] > j) hi = mid;
+                else lo = mid + 1;
+            }
+            const int64_t from = (int64_t)s_from[lo] + (j - (lo ? s_pref[lo - 1] : 0u));
+            const uint32_t at = carry + j;
+            const uint64_t x = from < n ? in[from] : 0ull;
+            if (in_lds) {
+                if (at < (uint32_t)BK_CAP) s_x[at] = x;
+            } else if (at < (uint32_t)size) {
+                X[at] = x;
+            }
+        }
+        carry += chunk;
+        __syncthreads();
+    }
+    if (in_lds) {
         const int wi = (int)ceil_div(size, 64 * BK_WAVES);
         const int base_at = wave * wi * 64 + lane;         // item k of this thread: base_at + 64 k
-        // LDS path: load, lpasses stable LDS passes, store
-#pragma unroll
-        for (int k = 0; k < BK_ITEMS; ++k) {
-            const int i = k * BK_THREADS + tid;
-            if (i < size) s_x[i] = in[start + i];
-        }
-        __syncthreads();
         uint64_t *src = s_x, *dst = s_y;
         for (int p = 0; p < lpasses; ++p) {
             uint64_t v[BK_ITEMS];
@@ -396,12 +553,9 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(uint64_t *__res
         }
         return;
     }
-
-    // global path: every pass counts the digits over the bucket, then places its
-    // chunks in order (stable), B -> A -> B ... with the last pass into out
-    uint64_t *src = in + start;
+    uint64_t *src = X;
     for (int p = 0; p < lpasses; ++p) {
-        uint64_t *dst = (p == lpasses - 1) ? out + start : ((p & 1) ? in + start : scratch + start);
+        uint64_t *dst = (p % 2 == 0) ? Y : X;
         const int shift = ebits + p * RADIX_BITS;
         for (int x = tid; x < RADIX; x += BK_THREADS) lstart[x] = 0;
         __syncthreads();
@@ -981,30 +1135,28 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
     if (!workspace || workspace_bytes < ws.bytes)
         return fail(GLSDM_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", what, ws.bytes,
                     workspace_bytes);
-    const unsigned prep_blocks = (unsigned)std::max<int64_t>(
-        std::min<int64_t>(ceil_div((int64_t)ws.status_words, 256), 4096), (MAX_PASSES * RADIX) / 256);
-    hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
-                       (int64_t)ws.status_words, ws.counter);
-    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), GLSDM_PACK_BLOCKS);
     int rc;
 #if GLSDM_BUCKET_SORT
     if (passes >= 3) {
-        // top address digit by one onesweep pass (a -> b), then each bucket by its block (b -> c)
+        // each tile orders its words by the top address digit (-> b, pieces in the
+        // look-back words' space), then each bucket gathers its pieces and sorts them (-> c)
         const int msd = ebits + abits - RADIX_BITS;
-        hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, msd, 1,
-                           entries, ws.a, ws.ghist);
-        if ((rc = check_launch("commit pack"))) return rc;
-        hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, ws.a, ws.b,
-                           entries, msd, ws.ghist, ws.status, ws.counter, ws.counter + MAX_PASSES);
-        if ((rc = check_launch("onesweep_kernel"))) return rc;
-        hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.a, ws.c, ws.ghist,
-                           ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
+        hipLaunchKernelGGL(tile_bucket_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, addresses, rows,
+                           ebits, msd, entries, ws.b, ws.status, ws.tiles, ws.counter);
+        if ((rc = check_launch("tile_bucket_kernel"))) return rc;
+        hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.status, ws.tiles,
+                           entries, ws.a, ws.c, ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
         sort_result(ws, passes, sorted, long_runs);
         *ebits_out = ebits;
         return GLSDM_OK;
     }
 #endif
+    const unsigned prep_blocks = (unsigned)std::max<int64_t>(
+        std::min<int64_t>(ceil_div((int64_t)ws.status_words, 256), 4096), (MAX_PASSES * RADIX) / 256);
+    hipLaunchKernelGGL(commit_prep_kernel, dim3(prep_blocks), dim3(256), 0, st, ws.ghist, ws.status,
+                       (int64_t)ws.status_words, ws.counter);
+    const unsigned pack_blocks = (unsigned)std::min<int64_t>(ceil_div(entries, 256), GLSDM_PACK_BLOCKS);
     hipLaunchKernelGGL(pack_hist_kernel, dim3(pack_blocks), dim3(256), 0, st, addresses, rows, ebits, ebits, passes,
                        entries, ws.a, ws.ghist);
     if ((rc = check_launch("commit pack"))) return rc;

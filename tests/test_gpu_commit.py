@@ -131,7 +131,7 @@ def test_commit_drops_out_of_range_addresses(device):
 
 @pytest.mark.parametrize("keyed", [False, True])
 @pytest.mark.parametrize("rows,D,E,lo,hi", [
-    (1 << 18, 32, 30000, 0, 1 << 18),        # three address digits: top-digit pass + per-bucket LDS sort
+    (1 << 18, 32, 30000, 0, 1 << 18),        # three address digits: tile bucketing + per-bucket LDS sort
     (1 << 20, 16, 60000, 0, 4096),           # one bucket holds every entry: chunked global bucket sort
     (1 << 20, 16, 50000, (1 << 20) - 3000, 1 << 20),   # a crowded last bucket plus the out-of-range run
     ((1 << 17) + 5, 8, 20000, 0, (1 << 17) + 5),
@@ -146,6 +146,21 @@ def test_commit_bucket_sort_paths(device, keyed, rows, D, E, lo, hi):
     out = hip.commit(flat.to(device), addr.to(device), delta.to(device), None if keys is None else keys.to(device))
     keep = addr < rows                                      # the oracle takes in-range entries only
     ref, _ = c_oracle.commit(flat, addr[keep], delta[keep], None if keys is None else keys[keep])
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_commit_bucket_sort_more_tiles_than_threads(device):
+    """Over 1024 sort tiles of 4096 entries: each bucket gathers its pieces in
+    several rounds, and every bucket (~17k words) takes the global-memory sort."""
+    rows, D, E = 1 << 20, 4, (1 << 22) + 200_003
+    g = torch.Generator().manual_seed(11)
+    flat = torch.randn(rows, D, generator=g)
+    addr = torch.randint(0, rows, (E,), generator=g)
+    addr[::9973] = rows + 1                                 # out of range: dropped
+    delta = torch.randn(E, D, generator=g) * 0.02
+    out = hip.commit(flat.to(device), addr.to(device), delta.to(device))
+    keep = addr < rows
+    ref, _ = c_oracle.commit(flat, addr[keep], delta[keep])
     assert torch.equal(out.cpu(), ref)
 
 
