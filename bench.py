@@ -52,10 +52,10 @@ CFG = CONFIGS[2]
 # WRITE x 1.0); source: profiles/glsdm_kernels.config2.hbm-traffic.md.  Re-measured
 # whenever a kernel of the path changes.
 TRAFFIC_PER_LAUNCH = {
-    "score_route": (5027.2 * 1.9998 + 6144.0) * 1024,
-    "read": (67332.5 * 1.9998 + 16384.0) * 1024,
-    "commit": ((10.7 + 2069.6 + 2260.2 + 2138.2 + 133293.2) * 1.9998
-               + (392.1 + 4224.0 + 4363.9 + 4097.5 + 120860.8)) * 1024,
+    "score_route": (5064.0 * 1.9998 + 10240.0) * 1024,
+    "read": (67334.1 * 1.9998 + 16384.0) * 1024,
+    # glsdm_commit on the bucket path: tile bucketing, bucket sort, segment
+    "commit": ((2122.0 + 2254.6 + 133294.0) * 1.9998 + (5120.1 + 4097.5 + 120860.8)) * 1024,
 }
 
 
@@ -628,9 +628,11 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=None,
                     help="config 5: decode steps (default 4096, the config's)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--schedule", choices=("serial", "overlap"), default="overlap",
-                    help="overlap (default): routes of later epochs on a second stream while the memory stream "
-                         "reads and commits; serial: every call on one stream")
+    ap.add_argument("--schedule", choices=("auto", "serial", "overlap"), default="auto",
+                    help="overlap: routes of later epochs on a second stream while the memory stream reads and "
+                         "commits; serial: every call on one stream; auto (default): overlap when a step has "
+                         "more than one epoch (with one, the next step's routes wait for this step's commit "
+                         "anyway, and the cross-stream waits only add latency)")
     ap.add_argument("--compare-schedules", action="store_true",
                     help="also time the other schedule (reported as ms_per_step_other_schedule)")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
@@ -664,13 +666,14 @@ def main():
         return
     cfg = CONFIGS[args.config]
     pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay")
+    if args.schedule == "auto":
+        args.schedule = "overlap" if pipe.epochs > 1 else "serial"
     unique = pipe.unique_rows()
-    for _ in range(args.warmup):
-        pipe.step()
-    torch.cuda.synchronize()
-
     run = pipe.step if args.schedule == "overlap" else pipe.step_serial
     other = pipe.step_serial if args.schedule == "overlap" else pipe.step
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
 
     # instrumented pass: events around every call, to find the dominant call
     pipe.timers = {}
@@ -738,7 +741,9 @@ def main():
     elif dominant == "commit":
         bytes_launch, t_launch = statistics.mean(commit_b), t_timed * 1e-3
         entry = "glsdm_commit_proposals" if args.write_path == "proposals" else "glsdm_commit"
-        roof = {"kernel": f"{entry} (prep + pack + top-digit pass + bucket sort + segment)", "bound": "hbm",
+        steps = ("tile bucketing + bucket sort + segment" if pipe.rows >= 1 << 16
+                 else "prep + pack + LSD passes + segment")
+        roof = {"kernel": f"{entry} ({steps})", "bound": "hbm",
                 "unit": "GB/s",
                 "peak": HBM_PEAK / 1e9}
         achieved = bytes_launch / t_launch / 1e9
