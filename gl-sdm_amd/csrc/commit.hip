@@ -62,6 +62,17 @@ constexpr int SORT_ITEMS = GLSDM_SORT_ITEMS;            // per thread
 constexpr int SORT_TILE = SORT_THREADS * SORT_ITEMS;    // entries per tile
 constexpr int SORT_WAVES = SORT_THREADS / 64;
 constexpr int WAVE_ITEMS = SORT_TILE / SORT_WAVES;      // consecutive entries per wave
+#ifndef GLSDM_BT_THREADS
+#define GLSDM_BT_THREADS 512
+#endif
+#ifndef GLSDM_BT_ITEMS
+#define GLSDM_BT_ITEMS 4
+#endif
+constexpr int BT_THREADS = GLSDM_BT_THREADS;           // bucket path, step 1: threads per tile (>= RADIX)
+constexpr int BT_ITEMS = GLSDM_BT_ITEMS;
+constexpr int BT_TILE = BT_THREADS * BT_ITEMS;
+constexpr int BT_WAVES = BT_THREADS / 64;
+constexpr int BT_WAVE_ITEMS = BT_TILE / BT_WAVES;
 constexpr int MAX_PASSES = 8;
 constexpr int64_t MAX_ENTRIES = (int64_t)1 << 30;       // look-back words hold 30-bit counts
 #ifndef GLSDM_SEG_WAVES
@@ -80,7 +91,7 @@ struct CommitWorkspace {
     uint32_t *ghist;    // [MAX_PASSES][RADIX] global digit counts
     uint32_t *status;   // [passes][tiles][RADIX] look-back words
     uint32_t *counter;  // [MAX_PASSES] tile-id counters, an error word, the deferred-run count
-    int64_t tiles;
+    int64_t tiles, bucket_tiles;
     size_t status_words;
     size_t bytes;
 };
@@ -89,7 +100,9 @@ static CommitWorkspace plan_workspace(void *base, int64_t entries, int passes)
 {
     CommitWorkspace w;
     w.tiles = ceil_div(entries, SORT_TILE);
-    w.status_words = (size_t)passes * (size_t)w.tiles * RADIX;
+    w.bucket_tiles = ceil_div(entries, BT_TILE);
+    // look-back words of the LSD passes, or the bucket path's piece words
+    w.status_words = std::max((size_t)passes * (size_t)w.tiles, (size_t)w.bucket_tiles) * RADIX;
     const size_t words = align256(sizeof(uint64_t) * (size_t)entries);
     const size_t ghist = align256(sizeof(uint32_t) * MAX_PASSES * RADIX);
     const size_t status = align256(sizeof(uint32_t) * w.status_words);
@@ -287,8 +300,11 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
 // result equals the full LSD sort.  A bucket of up to BK_CAP words is sorted
 // in LDS; a larger one (skewed addresses) in chunks of BK_CAP through global
 // scratch, with a counting pass per digit.
-constexpr int BK_THREADS = 1024;
-constexpr int BK_ITEMS = 8;
+#ifndef GLSDM_BK_THREADS
+#define GLSDM_BK_THREADS 1024
+#endif
+constexpr int BK_THREADS = GLSDM_BK_THREADS;
+constexpr int BK_ITEMS = 8192 / BK_THREADS;
 constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // 8192 words
 constexpr int BK_WAVES = BK_THREADS / 64;
 
@@ -337,38 +353,39 @@ __device__ __forceinline__ void bk_rank(const uint64_t (&v)[BK_ITEMS], const boo
     __syncthreads();                                      // the wave prefixes are read by every thread
 }
 
-// Bucket path, step 1: each tile of SORT_TILE consecutive entries packs its words, orders them stably by the top
-// address digit in LDS and stores them in that order at the tile's own
-// position, with one word per (digit, tile) -- the tile's first position of
+// Bucket path, step 1: each tile of BT_TILE consecutive entries packs its
+// words, orders them stably by the top address digit in LDS and stores them in
+// that order at the tile's own position, with one word per (digit, tile) -- the tile's first position of
 // the digit << 16 | the digit's count in the tile -- stored digit-major, so the
 // block that sorts a bucket reads its pieces of every tile in one coalesced
 // load.  Block 0 also clears the workspace's counter words.
-static_assert(SORT_TILE < 65536, "tile positions and counts are 16-bit");
+static_assert(BT_TILE < 65536 && BT_THREADS >= RADIX && BT_THREADS % 64 == 0,
+              "tile positions and counts are 16-bit; one thread per digit");
 
-__global__ __launch_bounds__(SORT_THREADS) void tile_bucket_kernel(const int64_t *__restrict__ addresses,
+__global__ __launch_bounds__(BT_THREADS) void tile_bucket_kernel(const int64_t *__restrict__ addresses,
                                                                    int64_t rows, int ebits, int shift, int64_t n,
                                                                    uint64_t *__restrict__ out,
                                                                    uint32_t *__restrict__ pieces, int64_t tiles,
                                                                    uint32_t *__restrict__ counter)
 {
-    __shared__ uint32_t cnt[SORT_WAVES][RADIX];
+    __shared__ uint32_t cnt[BT_WAVES][RADIX];
     __shared__ uint32_t s_wsum[RADIX / 64];
     __shared__ uint32_t lstart[RADIX];
-    __shared__ uint64_t s_items[SORT_TILE];
+    __shared__ uint64_t s_items[BT_TILE];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const bool owner = tid < RADIX;
     const int64_t tile = blockIdx.x;
     if (tile == 0 && tid < MAX_PASSES + 2) counter[tid] = 0;
-    for (int x = tid; x < SORT_WAVES * RADIX; x += SORT_THREADS) (&cnt[0][0])[x] = 0;
+    for (int x = tid; x < BT_WAVES * RADIX; x += BT_THREADS) (&cnt[0][0])[x] = 0;
     __syncthreads();
 
     // stable rank of each item among its wave's items of the same digit
     const uint64_t lt = (1ull << lane) - 1ull;
-    const int64_t start = tile * SORT_TILE + (int64_t)wave * WAVE_ITEMS;
-    uint64_t v[SORT_ITEMS];
-    uint32_t dig[SORT_ITEMS], pos[SORT_ITEMS];
+    const int64_t start = tile * BT_TILE + (int64_t)wave * BT_WAVE_ITEMS;
+    uint64_t v[BT_ITEMS];
+    uint32_t dig[BT_ITEMS], pos[BT_ITEMS];
 #pragma unroll
-    for (int k = 0; k < SORT_ITEMS; ++k) {
+    for (int k = 0; k < BT_ITEMS; ++k) {
         const int64_t i = start + k * 64 + lane;
         const bool valid = i < n;
         const int64_t a = valid ? addresses[i] : 0;
@@ -395,7 +412,7 @@ __global__ __launch_bounds__(SORT_THREADS) void tile_bucket_kernel(const int64_t
     uint32_t total = 0;
     if (owner) {
 #pragma unroll
-        for (int w = 0; w < SORT_WAVES; ++w) {
+        for (int w = 0; w < BT_WAVES; ++w) {
             const uint32_t x = cnt[w][tid];
             cnt[w][tid] = total;
             total += x;
@@ -408,18 +425,18 @@ __global__ __launch_bounds__(SORT_THREADS) void tile_bucket_kernel(const int64_t
     }
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < SORT_ITEMS; ++k) {
+    for (int k = 0; k < BT_ITEMS; ++k) {
         const int64_t i = start + k * 64 + lane;
         const uint32_t at = lstart[dig[k]] + cnt[wave][dig[k]] + pos[k];
-        if (i < n && at < (uint32_t)SORT_TILE) s_items[at] = v[k];
+        if (i < n && at < (uint32_t)BT_TILE) s_items[at] = v[k];
     }
     __syncthreads();
-    const int64_t tile_n = n - tile * SORT_TILE;
-    const int valid_items = tile_n < SORT_TILE ? (int)tile_n : SORT_TILE;
+    const int64_t tile_n = n - tile * BT_TILE;
+    const int valid_items = tile_n < BT_TILE ? (int)tile_n : BT_TILE;
 #pragma unroll
-    for (int k = 0; k < SORT_ITEMS; ++k) {
-        const int j = k * SORT_THREADS + tid;
-        if (j < valid_items) out[tile * SORT_TILE + j] = s_items[j];
+    for (int k = 0; k < BT_ITEMS; ++k) {
+        const int j = k * BT_THREADS + tid;
+        if (j < valid_items) out[tile * BT_TILE + j] = s_items[j];
     }
 }
 
@@ -498,7 +515,7 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(const uint64_t 
         uint32_t chunk;
         const uint32_t incl = block_scan(w & 0xffffu, s_scan, &chunk);   // its barriers end the last round's reads
         s_pref[tid] = incl;
-        s_from[tid] = (uint32_t)(t * SORT_TILE + (w >> 16));            // < n <= 2^30
+        s_from[tid] = (uint32_t)(t * BT_TILE + (w >> 16));              // < n <= 2^30
         __syncthreads();
         const int last = (int)(tiles - c0 < BK_THREADS ? tiles - c0 : BK_THREADS) - 1;
         for (uint32_t j = tid; j < chunk; j += BK_THREADS) {
@@ -1141,10 +1158,10 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
         // each tile orders its words by the top address digit (-> b, pieces in the
         // look-back words' space), then each bucket gathers its pieces and sorts them (-> c)
         const int msd = ebits + abits - RADIX_BITS;
-        hipLaunchKernelGGL(tile_bucket_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, addresses, rows,
-                           ebits, msd, entries, ws.b, ws.status, ws.tiles, ws.counter);
+        hipLaunchKernelGGL(tile_bucket_kernel, dim3((unsigned)ws.bucket_tiles), dim3(BT_THREADS), 0, st, addresses,
+                           rows, ebits, msd, entries, ws.b, ws.status, ws.bucket_tiles, ws.counter);
         if ((rc = check_launch("tile_bucket_kernel"))) return rc;
-        hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.status, ws.tiles,
+        hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.status, ws.bucket_tiles,
                            entries, ws.a, ws.c, ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
         sort_result(ws, passes, sorted, long_runs);
