@@ -44,11 +44,11 @@ class GlobalLayer(nn.Module):
         mass 1, with no averaging over tokens or layers; collisions commit in
         (address, position in chunk, layer) order through the keys.  Outside
         autograd the deltas stay deferred: the commit forms them from the rows
-        it touches.
+        it touches.  Under autograd (training with writes) they are
+        materialised as the reference does, so gradients flow through the
+        commit into later chunks' reads.
         """
-        if torch.is_grad_enabled() and x.requires_grad:
-            raise NotImplementedError("stack writes are forward-only on the HIP path: run the chunks that "
-                                      "commit under torch.no_grad() or torch.inference_mode()")
+        training = torch.is_grad_enabled() and (x.requires_grad or snapshot.values.requires_grad)
         B, T, _ = x.shape
         router = self.attn
         z = self.norm1(x)
@@ -59,4 +59,4 @@ class GlobalLayer(nn.Module):
         beta = router.beta(dense).float().sigmoid().unsqueeze(-1)
         log_decay = -F.softplus(router.decay(dense).float() - 4).unsqueeze(-1)
         return layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
-                              chunk_size, num_layers)
+                              chunk_size, num_layers, deferred=not training)

@@ -368,16 +368,42 @@ def proposal_keys(values, index, offset, chunk_size, num_layers, layer_idx):
     return addresses, keys
 
 
-def gather_rows(values, index):
-    """Rows ``[B, T, H, width, D]`` of the bank at ``index [B, T, H, width]``."""
-    addr = absolute_addresses(values, index)
-    device = values.device
+def _gather(values, addr, shape):
     D = values.shape[-1]
-    out = torch.empty((*index.shape, D), dtype=values.dtype, device=device)
-    rows = values.numel() // D
-    N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), rows, D, N.ptr(addr), addr.numel(),
-           N.ptr(out), N.stream(device))
+    out = torch.empty((*shape, D), dtype=values.dtype, device=values.device)
+    N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), values.numel() // D, D, N.ptr(addr),
+           addr.numel(), N.ptr(out), N.stream(values.device))
     return out
+
+
+class _GatherRows(torch.autograd.Function):
+    """The row gather of S/memory/routing.py:31-42; its backward adds each
+    gathered row's gradient onto its bank row, a row's terms summed in entry
+    order (the accumulating index backward of ``flat[address]``)."""
+
+    @staticmethod
+    def forward(ctx, values, index):
+        addr = absolute_addresses(values, index)
+        ctx.save_for_backward(addr)
+        ctx.values_shape, ctx.values_dtype = values.shape, values.dtype
+        return _gather(values, addr, index.shape)
+
+    @staticmethod
+    def backward(ctx, grad_rows):
+        (addr,) = ctx.saved_tensors
+        D = ctx.values_shape[-1]
+        grad_v = torch.zeros(ctx.values_shape, dtype=torch.float32, device=addr.device)
+        ones = torch.ones(addr.numel(), dtype=torch.float32, device=addr.device)
+        read_backward_rows(grad_v, addr.reshape(-1), ones, grad_rows.float().reshape(-1, D).contiguous())
+        return grad_v.to(ctx.values_dtype), None
+
+
+def gather_rows(values, index):
+    """Rows ``[B, T, H, width, D]`` of the bank at ``index [B, T, H, width]``;
+    differentiable w.r.t. ``values``."""
+    if torch.is_grad_enabled() and values.requires_grad:
+        return _GatherRows.apply(values, index)
+    return _gather(values, absolute_addresses(values, index), index.shape)
 
 
 def gather_flat(values, addresses):

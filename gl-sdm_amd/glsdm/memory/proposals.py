@@ -9,7 +9,8 @@ S/runtime/dense.py:11-14 against the snapshot rows the route selected (:44).
 ``deferred=True`` (default) returns a :class:`DeferredProposal`, whose deltas
 are evaluated inside the commit from the rows it touches (the ``[E, D]``
 deltas and the row re-gather are never materialised); ``deferred=False``
-returns the reference's :class:`WriteProposal` with fp32 deltas.
+returns the reference's :class:`WriteProposal` with fp32 deltas, which carry
+gradients under autograd.
 """
 import torch
 
@@ -28,7 +29,8 @@ def layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay
     if deferred:
         return DeferredProposal(snapshot.version, addresses, weights, prediction, target, beta, log_decay, mass,
                                 snapshot.lineage, keys)
+    from ..runtime.dense import proposal_delta          # autograd-aware (training with writes)
     rows = hip.gather_rows(snapshot.values, index)
-    delta = hip.proposal_delta(rows, weights, prediction, target, beta, log_decay, mass)
+    delta = proposal_delta(rows, weights, prediction, target, beta, log_decay, mass)
     return WriteProposal(snapshot.version, addresses.flatten(), delta.flatten(0, 3), snapshot.lineage,
                          keys.flatten())

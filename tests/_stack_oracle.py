@@ -50,7 +50,7 @@ def _commit(view, buffer, reference=False, backend="hip", donate=False):
     addr = torch.cat([p.addresses.cpu() for p in props])
     delta = torch.cat([p.deltas.cpu() for p in props])
     keys = torch.cat([p.sort_keys.cpu() for p in props])
-    flat = values.detach().cpu().float().reshape(-1, D)
+    flat = values.cpu().float().reshape(-1, D)      # differentiable, like the reference's commit
     new = torch_oracle.commit(flat, addr, delta, keys).to(values.dtype)
     return MemoryView(new.reshape(values.shape).to(values.device), view.version + 1, view.lineage)
 

@@ -74,6 +74,14 @@ def test_forward_only_guard():
     s = torch.zeros(2, 8, requires_grad=True)
     with pytest.raises(ValueError, match="CUDA"):
         hip.route(s, 2)
+    # the proposal arithmetic under autograd (training with writes) runs on the device only
+    from glsdm.runtime import proposal_delta
+    rows = torch.zeros(1, 2, 1, 2, 4, requires_grad=True)
+    with pytest.raises(ValueError, match="CUDA"):
+        proposal_delta(rows, torch.zeros(1, 2, 1, 2), torch.zeros(1, 2, 1, 4), torch.zeros(1, 2, 1, 4),
+                       torch.zeros(1, 2, 1, 1), torch.zeros(1, 2, 1, 1), torch.ones(1, 2))
+    with pytest.raises(ValueError, match="CUDA"):
+        hip.gather_rows(torch.zeros(1, 1, 4, 2, requires_grad=True), torch.zeros(1, 1, 1, 1, dtype=torch.int64))
 
 
 def test_bank_stays_fp32_and_caches_validate():
