@@ -229,3 +229,53 @@ def test_commit_proposals_config2_epoch(device):
         mass.reshape(-1)[r_idx // H].cpu(), decay=decay.reshape(-1)[r_idx].cpu().view(n, 1, 1))
     ref = torch_oracle.commit(compact, local, delta_c.view(n, D), all_keys[e_idx].cpu())
     assert torch.equal(fused.reshape(-1, D)[sel].cpu(), ref.to(torch.bfloat16))
+
+
+def test_materialised_proposals_commit_gradients(device):
+    """A read, two materialised proposals colliding at every address (the
+    second with doubled targets and mass 1 - m) and their commit under
+    autograd, with cotangents on both the reading and the committed bank: the
+    values and the gradients of the bank, route weights, targets, gates and
+    mass equal the reference's torch equations' (the protocol and tolerances
+    of P/tests/test_native_memory.py:52-93)."""
+    B, T, H, k, D, S = 2, 3, 2, 3, 37, 64
+    g = gen(91)
+    memory = torch.randn(B, H, S, D, generator=g)
+    index = torch.randint(0, S, (B, T, H, k), generator=g)
+    weights = torch.randn(B, T, H, k, generator=g).softmax(-1)
+    target = torch.randn(B, T, H, D, generator=g)
+    beta = torch.full((B, T, H, 1), 0.3)
+    log_decay = torch.full((B, T, H, 1), -0.12)
+    mass = torch.rand(B, T, generator=g)
+    read_cot, bank_cot = torch.randn(B, T, H, D, generator=g), torch.randn(B, H, S, D, generator=g)
+
+    def run(dev, native):
+        leaves = [t.to(dev).requires_grad_() for t in (memory, weights, target, beta, log_decay, mass)]
+        mem, w, tgt, b, ld, m = leaves
+        idx = index.to(dev)
+        if native:
+            view = MemoryView(mem)
+            read = hip.snapshot_read(mem, idx, w)
+            p1 = layer_proposal(view, idx, w, read, tgt, b, ld, 0, 0, T, 2, mass=m, deferred=False)
+            p2 = layer_proposal(view, idx, w, read, tgt * 2, b, ld, 0, 1, T, 2, mass=1 - m, deferred=False)
+            new = commit(view, merge(view, [p1, p2])).values
+        else:
+            read = torch_oracle.read(mem, idx, w)
+            rows = torch_oracle.gather_rows(mem, idx)
+            addr = torch_oracle.absolute_addresses(mem, idx)
+            pos = torch.arange(T).view(1, T, 1, 1)
+            d1 = torch_oracle.proposal_delta(rows, w, read, tgt, b, ld, m)
+            d2 = torch_oracle.proposal_delta(rows, w, read, tgt * 2, b, ld, 1 - m)
+            keys = torch.cat([(addr * (T * 2) + pos * 2 + layer).reshape(-1) for layer in (0, 1)])
+            new = torch_oracle.commit(mem.reshape(-1, D), torch.cat([addr.reshape(-1)] * 2),
+                                      torch.cat([d1.reshape(-1, D), d2.reshape(-1, D)]), keys).reshape(mem.shape)
+        loss = (read * read_cot.to(dev)).sum() + (new * bank_cot.to(dev)).sum()
+        grads = torch.autograd.grad(loss, leaves)
+        return [t.detach().cpu() for t in (read, new)], [t.cpu() for t in grads]
+
+    (read, new), grads = run(device, True)
+    (rread, rnew), rgrads = run("cpu", False)
+    torch.testing.assert_close(read, rread, atol=5e-7, rtol=2e-6)
+    torch.testing.assert_close(new, rnew, atol=1e-6, rtol=2e-6)
+    for name, actual, expected in zip(("memory", "weights", "target", "beta", "log_decay", "mass"), grads, rgrads):
+        torch.testing.assert_close(actual, expected, atol=2e-5, rtol=2e-5, msg=lambda m: f"{name}: {m}")

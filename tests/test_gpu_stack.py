@@ -193,6 +193,22 @@ def test_training_read_gradients_match_oracle(device):
     assert model.bank.memory.grad.abs().sum() > 0
 
 
+def test_delayed_write_gradients_for_every_global_layer(device):
+    """P/tests/test_layer_stack.py:64-82: a loss on the last token's hidden
+    state reaches the write projections of every global layer (through the
+    commits of the earlier chunks) and the learned bank."""
+    torch.manual_seed(7)
+    model = create_model(config()).to(device).train()
+    x = torch.randint(64, (1, 9), device=device)
+    model.hidden(x)[0][:, -1].square().sum().backward()
+    assert model.bank.memory.grad is not None
+    for block in model.blocks:
+        if isinstance(block, GlobalLayer):
+            for name in ("k", "v", "beta", "decay"):
+                gradient = getattr(block.attn, name).weight.grad
+                assert gradient is not None and torch.isfinite(gradient).all() and gradient.abs().sum() > 0, name
+
+
 @pytest.mark.parametrize("tokens", [12, 9])
 def test_training_write_gradients_match_oracle(device, tokens):
     """Three chunks of 4 tokens (the last one partial for 9): the first two
