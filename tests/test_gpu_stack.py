@@ -49,7 +49,9 @@ def rel_l2(a, b):
     config(),
     config(hidden_size=64, head_dim=32, gl_slots=64, gl_reads=4, gl_writes=4, gl_chunk_size=8,
            gl_local_window=8, num_hidden_layers=8, gl_layer_pattern=["local", "global"]),
-], ids=["tiny", "small"])
+    # P/tests/test_layer_stack.py:180-186: the large route (2^18 slots, 8 reads and writes)
+    config(gl_slots=262144, gl_reads=8, gl_writes=8),
+], ids=["tiny", "small", "large_route"])
 def test_stack_prefill_matches_oracle_memory(device, cfg):
     model, oracle = models(cfg, device)
     x = torch.randint(cfg["vocab_size"], (2, 23), generator=torch.Generator().manual_seed(0)).to(device)
@@ -121,8 +123,10 @@ def test_chunk_snapshot_is_shared_across_depth_and_local_history_survives_commit
     assert cache[0].local[0]["tokens"] == 9 and cache[0].local[0]["k"].shape[2] == 5
 
 
-def test_decode_continues_prefill(device):
-    model, _ = models(config(), device)
+@pytest.mark.parametrize("cfg", [config(), config(gl_slots=262144, gl_reads=8, gl_writes=8)],
+                         ids=["tiny", "large_route"])
+def test_decode_continues_prefill(device, cfg):
+    model, _ = models(cfg, device)
     x = torch.randint(64, (2, 21), generator=torch.Generator().manual_seed(3)).to(device)
     full, full_cache = model.prefill(x)
     first, cache = model.prefill(x[:, :17])
