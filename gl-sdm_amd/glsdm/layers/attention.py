@@ -8,10 +8,30 @@ positions, scaled dot-product attention over a rolling window, and a sigmoid
 output gate before ``proj``.  The KV cache keeps the last ``window - 1`` keys
 and values and the absolute token count, so chunked prefill and decode see
 exactly the keys a full pass sees.
+
+On the GPU outside autograd, the QK normalisation and rotary run as one HIP
+kernel per projection (``glsdm_qk_norm_rotary``) that also writes the
+``[B, heads, T, dk]`` layout; under autograd and on the CPU the same
+operations run as tensor ops.
 """
 import torch
 from torch import nn
 import torch.nn.functional as F
+
+from .. import _native as N
+
+
+def qk_norm_rotary(x, freq, offset):
+    """``rotary(F.rms_norm(x, (dk,)), offset).transpose(1, 2)`` for ``x [B, T, heads, dk]``
+    (fp32 or bf16, rows of dk contiguous elements at a uniform row stride) in one
+    HIP launch; returns ``[B, heads, T, dk]`` contiguous."""
+    B, T, heads, dk = x.shape
+    if not (x.stride(3) == 1 and x.stride(1) == heads * x.stride(2) and x.stride(0) == T * x.stride(1)):
+        x = x.contiguous()
+    out = torch.empty((B, heads, T, dk), dtype=x.dtype, device=x.device)
+    N.call("glsdm_qk_norm_rotary", N.ptr(x), N.dtype_code(x), B, T, heads, dk, x.stride(2), N.ptr(freq), offset,
+           N.ptr(out), N.stream(x.device))
+    return out
 
 
 class Transformer(nn.Module):
@@ -59,8 +79,14 @@ class Transformer(nn.Module):
         v = self.v(x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
         previous = cache["k"].shape[2] if cache else 0
         offset = 0 if cache is None else cache.get("tokens", previous)
-        q = self.rotary(F.rms_norm(q, (dk,)), offset).transpose(1, 2)
-        k = self.rotary(F.rms_norm(k, (dk,)), offset).transpose(1, 2)
+        fused = (x.is_cuda and dk <= 256 and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
+                 and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad)))
+        if fused:
+            freq = self.angular_freq.float().contiguous()
+            q, k = qk_norm_rotary(q, freq, offset), qk_norm_rotary(k, freq, offset)
+        else:
+            q = self.rotary(F.rms_norm(q, (dk,)), offset).transpose(1, 2)
+            k = self.rotary(F.rms_norm(k, (dk,)), offset).transpose(1, 2)
         if cache is not None:
             if cache:
                 k, v = torch.cat((cache["k"], k), 2), torch.cat((cache["v"], v), 2)

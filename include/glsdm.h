@@ -373,6 +373,20 @@ int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, int64_t H, 
 int glsdm_overlay_materialise(const void *base, int32_t dtype, const int32_t *map, const void *pool,
                               int64_t B, int64_t H, int64_t S, int64_t D, void *out, void *stream);
 
+/*
+ * QK normalisation and rotary positions of a local attention layer, fused:
+ * per head row x (dk elements at x + r*row_stride, r = (b*T + t)*heads + h),
+ * y = x*rsqrt(mean(x^2) + FLT_EPSILON) rounded to dtype, then with
+ * a = y[:dk/2], b = y[dk/2:], theta_j = (offset + t)*freq[j] (fp32, freq has
+ * dk/2 entries): cat(a cos + b sin, -a sin + b cos) rounded to dtype, written
+ * to out [B, heads, T, dk] contiguous.  dk a multiple of 4, at most 256;
+ * offset + T <= 2^24.
+ * Replaces: F.rms_norm(q|k, (head_dim,)) and Transformer.rotary, then
+ * .transpose(1, 2), of S/layers/attention.py:38-42,51-52.
+ */
+int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int64_t heads, int64_t dk,
+                         int64_t row_stride, const float *freq, int64_t offset, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,59 @@
+"""The fused QK normalisation + rotary kernel vs the local attention's tensor
+ops (S/layers/attention.py:38-42,51-52: F.rms_norm, then the rotary in fp32),
+run by PyTorch on the same device.
+
+Tolerances: fp32 within a few ulp (the mean's summation order and rsqrt may
+differ from PyTorch's kernels).  bf16: a last-bit difference of the fp32
+scale can round a normalised value (|y| < 8 here) the other way, which moves
+the outputs built from it by up to one bf16 ulp of y (2^-5) -- rare, so the
+fraction of differing outputs is bounded as well."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from glsdm.layers.attention import Transformer, qk_norm_rotary
+
+pytestmark = pytest.mark.gpu
+
+
+def _reference(x, freq, offset):
+    layer = Transformer.__new__(Transformer)
+    torch.nn.Module.__init__(layer)
+    layer.angular_freq = freq
+    return layer.rotary(F.rms_norm(x, (x.shape[-1],)), offset).transpose(1, 2)
+
+
+def _freq(dk, device):
+    rising = torch.pow(torch.tensor(1 / 1024), torch.linspace(0, 1, dk // 4))
+    return torch.cat((rising, torch.zeros_like(rising))).to(device)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,heads,dk,offset,strided", [
+    (2, 37, 16, 64, 0, True), (1, 5, 4, 16, 3, False), (3, 64, 8, 128, 511, True), (1, 9, 2, 256, 100000, False),
+    (4, 512, 16, 64, 7680, True), (1, 1, 1, 4, 0, False), (64, 1, 16, 64, 4095, True),
+])
+def test_qk_norm_rotary_matches_tensor_ops(device, dtype, B, T, heads, dk, offset, strided):
+    g = torch.Generator().manual_seed(B * 1000 + T + dk)
+    if strided:   # the query half of a [query | gate] projection, as the layer sees it
+        x = (torch.randn(B, T, heads, 2 * dk, generator=g) * 3).to(dtype).to(device).chunk(2, -1)[0]
+    else:
+        x = (torch.randn(B, T, heads, dk, generator=g) * 3).to(dtype).to(device)
+    freq = _freq(dk, device)
+    out = qk_norm_rotary(x, freq, offset)
+    ref = _reference(x, freq, offset)
+    assert out.shape == ref.shape and out.dtype == dtype and out.is_contiguous()
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, ref, atol=1e-6, rtol=1e-5)
+    else:
+        torch.testing.assert_close(out.float(), ref.float(), atol=2 ** -5, rtol=2 ** -7)
+        assert (out != ref).float().mean().item() < 1e-4
+
+
+def test_qk_norm_rotary_rejects_bad_shapes(device):
+    from glsdm import _native as N
+    x = torch.zeros(1, 2, 1, 6, device=device)
+    with pytest.raises(ValueError):
+        qk_norm_rotary(x, _freq(8, device)[:3], 0)            # dk not a multiple of 4
+    with pytest.raises((ValueError, RuntimeError)):
+        N.call("glsdm_qk_norm_rotary", N.ptr(x), 0, 1, 2, 1, 512, 512, N.ptr(x), 0, N.ptr(x), N.stream(device))
