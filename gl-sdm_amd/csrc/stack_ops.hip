@@ -8,10 +8,13 @@
 //   with a = y[:dk/2], b = y[dk/2:] in fp32 and theta_j = (offset + t) * freq[j]:
 //   out = cat(a cos(theta) + b sin(theta), -a sin(theta) + b cos(theta)),
 //       rounded to the row dtype,
-// every product and sum a separate fp32 operation in that order.  One
-// wavefront per row; rows are read through a row stride (the query half is a
-// strided view) and written [B, heads, T, dk] contiguous, the layout
-// attention and the KV cache take, so the transposes disappear as well.
+// every product and sum a separate fp32 operation in that order.  One block
+// per token (b, t): its threads first put cos/sin of the token's dk/2 angles
+// in LDS (shared by all heads), then take the heads' rows, dk/4 lanes per row,
+// each lane two consecutive (a, b) pairs; the row's sum of squares is reduced
+// over its lanes with shuffles.  Rows are read through a row stride (the
+// query half is a strided view) and written [B, heads, T, dk] contiguous, the
+// layout attention and the KV cache take, so the transposes disappear too.
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -28,77 +31,148 @@ template <> struct RowIO<bf16_t> {
     __device__ __forceinline__ static void store(bf16_t *p, float v) { *p = f32_to_bf16(v); }
 };
 
-constexpr int QK_MAX_PAIRS = 2;          // dk <= 256: each lane takes up to two (a, b) pairs
+constexpr int QK_THREADS = 256;
+constexpr int QK_MAX_DK = 256;
 
-template <typename TX>
-__global__ __launch_bounds__(256) void qk_norm_rotary_kernel(const TX *__restrict__ x, int64_t row_stride,
-                                                             int64_t rows, int64_t T, int64_t heads, int dk,
-                                                             const float *__restrict__ freq, int64_t offset,
-                                                             TX *__restrict__ out)
+template <typename TX, int L>   // L = dk / 4 lanes per row, a power of two <= 64
+__global__ __launch_bounds__(QK_THREADS) void qk_norm_rotary_kernel(const TX *__restrict__ x, int64_t row_stride,
+                                                                    int64_t T, int64_t heads,
+                                                                    const float *__restrict__ freq, int64_t offset,
+                                                                    TX *__restrict__ out)
 {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int64_t r = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (r >= rows) return;                                  // wave-uniform
-    const int half = dk >> 1;
-    const TX *src = x + r * row_stride;
-    float a[QK_MAX_PAIRS], b[QK_MAX_PAIRS];
-    float ss = 0.0f;
-#pragma unroll
-    for (int p = 0; p < QK_MAX_PAIRS; ++p) {
-        const int j = lane + 64 * p;
-        a[p] = j < half ? RowIO<TX>::load(src + j) : 0.0f;
-        b[p] = j < half ? RowIO<TX>::load(src + half + j) : 0.0f;
-        ss += a[p] * a[p];
-        ss += b[p] * b[p];
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    const float scale = rsqrtf(ss / (float)dk + __FLT_EPSILON__);
-    // row r = (bt * heads + h) with bt = batch * T + t
-    const int64_t h = r % heads, bt = r / heads;
+    constexpr int dk = 4 * L, half = 2 * L, rows_per_pass = QK_THREADS / L;
+    __shared__ float s_cos[QK_MAX_DK / 2], s_sin[QK_MAX_DK / 2];
+    const int64_t bt = blockIdx.x;                          // token b*T + t
     const int64_t t = bt % T, batch = bt / T;
-    TX *dst = out + ((batch * heads + h) * T + t) * dk;
-    const float pos = (float)(offset + t);
-#pragma unroll
-    for (int p = 0; p < QK_MAX_PAIRS; ++p) {
-        const int j = lane + 64 * p;
-        if (j >= half) continue;
-        const float ya = RowIO<TX>::round(a[p] * scale), yb = RowIO<TX>::round(b[p] * scale);
-        const float theta = pos * freq[j];
-        const float c = cosf(theta), s = sinf(theta);
-        const float ac = ya * c, bs = yb * s;
-        const float na = -ya;
-        const float as = na * s, bc = yb * c;
-        RowIO<TX>::store(dst + j, ac + bs);
-        RowIO<TX>::store(dst + half + j, as + bc);
+    const int tid = threadIdx.x;
+    if (tid < half) {
+        const float theta = (float)(offset + t) * freq[tid];
+        s_cos[tid] = cosf(theta);
+        s_sin[tid] = sinf(theta);
     }
+    __syncthreads();
+    const int li = tid % L, j = 2 * li;
+    for (int64_t h = tid / L; h < heads; h += rows_per_pass) {     // uniform within a row's lanes
+        const TX *src = x + (bt * heads + h) * row_stride;
+        float a0 = RowIO<TX>::load(src + j), a1 = RowIO<TX>::load(src + j + 1);
+        float b0 = RowIO<TX>::load(src + half + j), b1 = RowIO<TX>::load(src + half + j + 1);
+        float ss = a0 * a0;
+        ss += a1 * a1;
+        ss += b0 * b0;
+        ss += b1 * b1;
+#pragma unroll
+        for (int off = L / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        const float scale = rsqrtf(ss / (float)dk + __FLT_EPSILON__);
+        a0 = RowIO<TX>::round(a0 * scale);
+        a1 = RowIO<TX>::round(a1 * scale);
+        b0 = RowIO<TX>::round(b0 * scale);
+        b1 = RowIO<TX>::round(b1 * scale);
+        TX *dst = out + ((batch * heads + h) * T + t) * dk;
+        const float c0 = s_cos[j], c1 = s_cos[j + 1], s0 = s_sin[j], s1 = s_sin[j + 1];
+        const float ac0 = a0 * c0, bs0 = b0 * s0, ac1 = a1 * c1, bs1 = b1 * s1;
+        const float as0 = (-a0) * s0, bc0 = b0 * c0, as1 = (-a1) * s1, bc1 = b1 * c1;
+        RowIO<TX>::store(dst + j, ac0 + bs0);
+        RowIO<TX>::store(dst + j + 1, ac1 + bs1);
+        RowIO<TX>::store(dst + half + j, as0 + bc0);
+        RowIO<TX>::store(dst + half + j + 1, as1 + bc1);
+    }
+}
+
+template <typename TX>
+static void launch_qk(const void *x, int64_t row_stride, int64_t tokens, int64_t T, int64_t heads, int64_t dk,
+                      const float *freq, int64_t offset, void *out, hipStream_t st)
+{
+    const TX *xp = static_cast<const TX *>(x);
+    TX *op = static_cast<TX *>(out);
+    const dim3 grid((unsigned)tokens), block(QK_THREADS);
+#define GLSDM_QK(LANES)                                                                                       \
+    hipLaunchKernelGGL((qk_norm_rotary_kernel<TX, LANES>), grid, block, 0, st, xp, row_stride, T, heads, freq, \
+                       offset, op)
+    switch (dk / 4) {
+    case 1: GLSDM_QK(1); break;
+    case 2: GLSDM_QK(2); break;
+    case 4: GLSDM_QK(4); break;
+    case 8: GLSDM_QK(8); break;
+    case 16: GLSDM_QK(16); break;
+    case 32: GLSDM_QK(32); break;
+    default: GLSDM_QK(64); break;
+    }
+#undef GLSDM_QK
+}
+
+// The attention output's gate (S/layers/attention.py:77, before proj):
+// out[b, t, h*dk + i] = o[b, h, t, i] * sigmoid(gate[b, t, h, i]), with the
+// sigmoid 1 / (1 + exp(-g)) in fp32 rounded to the dtype, then the product
+// rounded to the dtype.  o and gate are read through their strides (SDPA's
+// output and the gate half of the [query | gate] projection); out is
+// [B, T, H*dk] contiguous, the input of proj.  One thread per element.
+template <typename TX>
+__global__ __launch_bounds__(256) void gate_merge_kernel(const TX *__restrict__ o, int64_t os0, int64_t os1,
+                                                         int64_t os2, const TX *__restrict__ gate, int64_t gs0,
+                                                         int64_t gs1, int64_t gs2, int64_t T, int64_t H, int64_t dk,
+                                                         int64_t n, TX *__restrict__ out)
+{
+#pragma clang fp contract(off)
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int64_t i = e % dk, r = e / dk;                   // r = (b*T + t)*H + h
+    const int64_t h = r % H, bt = r / H;
+    const int64_t t = bt % T, b = bt / T;
+    const float g = RowIO<TX>::load(gate + b * gs0 + t * gs1 + h * gs2 + i);
+    const float sig = RowIO<TX>::round(1.0f / (1.0f + expf(-g)));
+    const float v = RowIO<TX>::load(o + b * os0 + h * os1 + t * os2 + i);
+    RowIO<TX>::store(out + e, v * sig);
 }
 
 }  // namespace glsdm
 
 using namespace glsdm;
 
+extern "C" int glsdm_gate_merge(const void *o, const int64_t *o_strides, const void *gate, const int64_t *gate_strides,
+                                int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t dk, void *out, void *stream)
+{
+    if (B < 0 || T < 0 || H < 1 || dk < 1) return fail(GLSDM_ERR_ARG, "gate_merge: bad shape");
+    if (!dtype_ok(dtype)) return fail(GLSDM_ERR_ARG, "gate_merge: bad dtype");
+    const int64_t n = B * T * H * dk;
+    if (n == 0) return GLSDM_OK;
+    if (!o || !o_strides || !gate || !gate_strides || !out) return fail(GLSDM_ERR_ARG, "gate_merge: null pointer");
+    if (o_strides[3] != 1 || gate_strides[3] != 1)
+        return fail(GLSDM_ERR_UNSUPPORTED, "gate_merge: the last dimension must be contiguous");
+    if (ceil_div(n, 256) > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "gate_merge: too many elements");
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
+    if (dtype == GLSDM_F32)
+        hipLaunchKernelGGL(gate_merge_kernel<float>, grid, block, 0, st, static_cast<const float *>(o), o_strides[0],
+                           o_strides[1], o_strides[2], static_cast<const float *>(gate), gate_strides[0],
+                           gate_strides[1], gate_strides[2], T, H, dk, n, static_cast<float *>(out));
+    else
+        hipLaunchKernelGGL(gate_merge_kernel<bf16_t>, grid, block, 0, st, static_cast<const bf16_t *>(o),
+                           o_strides[0], o_strides[1], o_strides[2], static_cast<const bf16_t *>(gate),
+                           gate_strides[0], gate_strides[1], gate_strides[2], T, H, dk, n,
+                           static_cast<bf16_t *>(out));
+    return check_launch("gate_merge_kernel");
+}
+
 extern "C" int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int64_t heads, int64_t dk,
                                     int64_t row_stride, const float *freq, int64_t offset, void *out, void *stream)
 {
-    if (B < 0 || T < 0 || heads < 1 || dk < 4 || dk % 4 != 0 || dk > 64 * 2 * QK_MAX_PAIRS || row_stride < dk ||
-        offset < 0)
-        return fail(GLSDM_ERR_ARG, "qk_norm_rotary: bad shape B=%lld T=%lld heads=%lld dk=%lld stride=%lld",
-                    (long long)B, (long long)T, (long long)heads, (long long)dk, (long long)row_stride);
+    const bool pow2 = dk >= 4 && dk <= QK_MAX_DK && (dk & (dk - 1)) == 0;
+    if (B < 0 || T < 0 || heads < 1 || !pow2 || row_stride < dk || offset < 0)
+        return fail(GLSDM_ERR_ARG, "qk_norm_rotary: bad shape B=%lld T=%lld heads=%lld dk=%lld stride=%lld "
+                    "(dk a power of two in [4, 256])", (long long)B, (long long)T, (long long)heads, (long long)dk,
+                    (long long)row_stride);
     if (!dtype_ok(dtype)) return fail(GLSDM_ERR_ARG, "qk_norm_rotary: bad dtype");
     if (offset + T > (int64_t)1 << 24)
         return fail(GLSDM_ERR_UNSUPPORTED, "qk_norm_rotary: positions above 2^24 are not exact in fp32");
-    const int64_t rows = B * T * heads;
-    if (rows == 0) return GLSDM_OK;
+    const int64_t tokens = B * T;
+    if (tokens == 0) return GLSDM_OK;
+    if (tokens > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "qk_norm_rotary: more than 2^31-1 tokens");
     if (!x || !freq || !out) return fail(GLSDM_ERR_ARG, "qk_norm_rotary: null pointer");
     const hipStream_t st = as_stream(stream);
-    const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
     if (dtype == GLSDM_F32)
-        hipLaunchKernelGGL(qk_norm_rotary_kernel<float>, grid, block, 0, st, static_cast<const float *>(x), row_stride,
-                           rows, T, heads, (int)dk, freq, offset, static_cast<float *>(out));
+        launch_qk<float>(x, row_stride, tokens, T, heads, dk, freq, offset, out, st);
     else
-        hipLaunchKernelGGL(qk_norm_rotary_kernel<bf16_t>, grid, block, 0, st, static_cast<const bf16_t *>(x),
-                           row_stride, rows, T, heads, (int)dk, freq, offset, static_cast<bf16_t *>(out));
+        launch_qk<bf16_t>(x, row_stride, tokens, T, heads, dk, freq, offset, out, st);
     return check_launch("qk_norm_rotary_kernel");
 }

@@ -14,6 +14,8 @@ kernel per projection (``glsdm_qk_norm_rotary``) that also writes the
 ``[B, heads, T, dk]`` layout; under autograd and on the CPU the same
 operations run as tensor ops.
 """
+import ctypes
+
 import torch
 from torch import nn
 import torch.nn.functional as F
@@ -32,6 +34,40 @@ def qk_norm_rotary(x, freq, offset):
     N.call("glsdm_qk_norm_rotary", N.ptr(x), N.dtype_code(x), B, T, heads, dk, x.stride(2), N.ptr(freq), offset,
            N.ptr(out), N.stream(x.device))
     return out
+
+
+def gate_merge(o, gate):
+    """``o.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid()`` for
+    ``o [B, H, T, dk]`` and ``gate [B, T, H, dk]`` (any strides with contiguous
+    rows) in one HIP launch."""
+    B, H, T, dk = o.shape
+    out = torch.empty((B, T, H * dk), dtype=o.dtype, device=o.device)
+    os_, gs = (ctypes.c_int64 * 4)(*o.stride()), (ctypes.c_int64 * 4)(*gate.stride())
+    N.call("glsdm_gate_merge", N.ptr(o), os_, N.ptr(gate), gs, N.dtype_code(o), B, T, H, dk, N.ptr(out),
+           N.stream(o.device))
+    return out
+
+
+_MASKS = {}
+
+
+def _window_mask(previous, T, window, device):
+    """Query i (position offset + i) may see key j (position offset - previous + j)
+    when the key is not later and, with a window, less than ``window`` back.  It
+    depends on (previous, T, window) only, not on the offset, so one tensor per
+    shape is kept (prefill chunks and decode steps reuse it)."""
+    key = (previous, T, window, device)
+    mask = _MASKS.get(key)
+    if mask is None:
+        kpos = torch.arange(-previous, T, device=device)[None, :]
+        qpos = torch.arange(0, T, device=device)[:, None]
+        mask = kpos <= qpos
+        if window is not None:
+            mask = mask & (kpos > qpos - window)
+        if len(_MASKS) >= 64:
+            _MASKS.clear()
+        _MASKS[key] = mask
+    return mask
 
 
 class Transformer(nn.Module):
@@ -79,7 +115,7 @@ class Transformer(nn.Module):
         v = self.v(x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
         previous = cache["k"].shape[2] if cache else 0
         offset = 0 if cache is None else cache.get("tokens", previous)
-        fused = (x.is_cuda and dk <= 256 and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
+        fused = (x.is_cuda and dk in (4, 8, 16, 32, 64, 128, 256) and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
                  and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad)))
         if fused:
             freq = self.angular_freq.float().contiguous()
@@ -100,10 +136,9 @@ class Transformer(nn.Module):
         # needs this offset causal mask (SDPA's own causal mask is upper-left aligned)
         mask = None
         if offset or self.window is not None:
-            kpos = torch.arange(offset - previous, offset + T, device=x.device)[None, :]
-            qpos = torch.arange(offset, offset + T, device=x.device)[:, None]
-            mask = kpos <= qpos
-            if self.window is not None:
-                mask = mask & (kpos > qpos - self.window)
+            mask = _window_mask(previous, T, self.window, x.device)
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
+        if fused and out.stride(-1) == 1 and gate.stride(-1) == 1 and not (
+                torch.is_grad_enabled() and (out.requires_grad or gate.requires_grad)):
+            return self.proj(gate_merge(out, gate))
         return self.proj(out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid())

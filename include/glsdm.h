@@ -379,13 +379,25 @@ int glsdm_overlay_materialise(const void *base, int32_t dtype, const int32_t *ma
  * y = x*rsqrt(mean(x^2) + FLT_EPSILON) rounded to dtype, then with
  * a = y[:dk/2], b = y[dk/2:], theta_j = (offset + t)*freq[j] (fp32, freq has
  * dk/2 entries): cat(a cos + b sin, -a sin + b cos) rounded to dtype, written
- * to out [B, heads, T, dk] contiguous.  dk a multiple of 4, at most 256;
+ * to out [B, heads, T, dk] contiguous.  dk a power of two in [4, 256];
  * offset + T <= 2^24.
  * Replaces: F.rms_norm(q|k, (head_dim,)) and Transformer.rotary, then
  * .transpose(1, 2), of S/layers/attention.py:38-42,51-52.
  */
 int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int64_t heads, int64_t dk,
                          int64_t row_stride, const float *freq, int64_t offset, void *out, void *stream);
+
+/*
+ * The gated attention output: out[b, t, h*dk + i] = o[b, h, t, i] *
+ * sigmoid(gate[b, t, h, i]) (sigmoid in fp32 rounded to dtype, then the
+ * product rounded to dtype), o [B, H, T, dk] and gate [B, T, H, dk] read
+ * through their element strides (4 each, last one 1), out [B, T, H*dk]
+ * contiguous.
+ * Replaces: out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid()
+ * of S/layers/attention.py:77.
+ */
+int glsdm_gate_merge(const void *o, const int64_t *o_strides, const void *gate, const int64_t *gate_strides,
+                     int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t dk, void *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -57,3 +57,22 @@ def test_qk_norm_rotary_rejects_bad_shapes(device):
         qk_norm_rotary(x, _freq(8, device)[:3], 0)            # dk not a multiple of 4
     with pytest.raises((ValueError, RuntimeError)):
         N.call("glsdm_qk_norm_rotary", N.ptr(x), 0, 1, 2, 1, 512, 512, N.ptr(x), 0, N.ptr(x), N.stream(device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,T,dk", [(2, 16, 37, 64), (1, 4, 5, 16), (4, 16, 512, 64), (64, 16, 1, 64),
+                                      (3, 2, 9, 12)])
+def test_gate_merge_matches_tensor_ops(device, dtype, B, H, T, dk):
+    """The attention output's gate (S/layers/attention.py:77) bit for bit: the
+    same fp32 sigmoid rounded to the dtype, then one rounded product."""
+    from glsdm.layers.attention import gate_merge
+    g = torch.Generator().manual_seed(B * 100 + T)
+    o = (torch.randn(B, T, H, dk, generator=g)).to(dtype).to(device).transpose(1, 2)   # strided, as SDPA may give
+    proj = (torch.randn(B, T, H, 2 * dk, generator=g) * 4).to(dtype).to(device)
+    gate = proj.chunk(2, -1)[1]
+    out = gate_merge(o, gate)
+    ref = o.transpose(1, 2).reshape(B, T, H * dk) * gate.reshape(B, T, H * dk).sigmoid()
+    assert out.shape == ref.shape and out.dtype == dtype
+    torch.testing.assert_close(out, ref, atol=0, rtol=0)
+    out2 = gate_merge(o.contiguous(), gate)
+    torch.testing.assert_close(out2, ref, atol=0, rtol=0)
