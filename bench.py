@@ -55,7 +55,7 @@ TRAFFIC_PER_LAUNCH = {
     "score_route": (5064.0 * 1.9998 + 10240.0) * 1024,
     "read": (67334.1 * 1.9998 + 16384.0) * 1024,
     # glsdm_commit on the bucket path: tile bucketing, bucket sort, segment
-    "commit": ((2122.0 + 2254.6 + 133294.0) * 1.9998 + (5120.1 + 4097.5 + 120860.8)) * 1024,
+    "commit": ((2093.6 + 2375.2 + 133295.0) * 1.9998 + (6144.1 + 4097.5 + 120860.8)) * 1024,
 }
 
 
