@@ -125,9 +125,95 @@ __global__ __launch_bounds__(256) void gate_merge_kernel(const TX *__restrict__ 
     RowIO<TX>::store(out + e, v * sig);
 }
 
+// The MLP's activation (S/layers/common.py:19-27): with u, g the two halves of
+// each row of fc(x) [rows, 2*inner], out = g * relu(u)^2, the square rounded
+// to the dtype, then the product rounded to the dtype (the tensor ops'
+// roundings).  VEC elements (16 bytes) per thread, inner a multiple of VEC.
+template <typename TX> struct Vec16;
+template <> struct Vec16<float> {
+    static constexpr int N = 4;
+    typedef float4 Raw;
+    __device__ __forceinline__ static void unpack(const Raw &r, float (&v)[N])
+    {
+        v[0] = r.x;
+        v[1] = r.y;
+        v[2] = r.z;
+        v[3] = r.w;
+    }
+    __device__ __forceinline__ static Raw pack(const float (&v)[N]) { return make_float4(v[0], v[1], v[2], v[3]); }
+};
+template <> struct Vec16<bf16_t> {
+    static constexpr int N = 8;
+    typedef uint4 Raw;
+    __device__ __forceinline__ static void unpack(const Raw &r, float (&v)[N])
+    {
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = bf16_to_f32((bf16_t)(w[i] & 0xFFFFu));
+            v[2 * i + 1] = bf16_to_f32((bf16_t)(w[i] >> 16));
+        }
+    }
+    __device__ __forceinline__ static Raw pack(const float (&v)[N])
+    {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+        return make_uint4(w[0], w[1], w[2], w[3]);
+    }
+};
+
+template <typename TX>
+__global__ __launch_bounds__(256) void relu2_gate_kernel(const TX *__restrict__ fc, int64_t rows, int64_t inner,
+                                                         TX *__restrict__ out)
+{
+#pragma clang fp contract(off)
+    using V = Vec16<TX>;
+    const int64_t per_row = inner / V::N;
+    const int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= rows * per_row) return;
+    const int64_t r = v / per_row, c = (v % per_row) * V::N;
+    const TX *row = fc + r * 2 * inner;
+    float u[V::N], g[V::N], o[V::N];
+    V::unpack(*reinterpret_cast<const typename V::Raw *>(row + c), u);
+    V::unpack(*reinterpret_cast<const typename V::Raw *>(row + inner + c), g);
+#pragma unroll
+    for (int i = 0; i < V::N; ++i) {
+        const float relu = (u[i] > 0.0f || u[i] != u[i]) ? u[i] : 0.0f;   // relu keeps NaN
+        const float sq = RowIO<TX>::round(relu * relu);
+        o[i] = g[i] * sq;
+    }
+    *reinterpret_cast<typename V::Raw *>(out + r * inner + c) = V::pack(o);
+}
+
 }  // namespace glsdm
 
 using namespace glsdm;
+
+extern "C" int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner, void *out, void *stream)
+{
+    if (rows < 0 || inner < 1) return fail(GLSDM_ERR_ARG, "relu2_gate: bad shape");
+    if (!dtype_ok(dtype)) return fail(GLSDM_ERR_ARG, "relu2_gate: bad dtype");
+    const int vec = dtype == GLSDM_F32 ? 4 : 8;
+    if (inner % vec != 0) return fail(GLSDM_ERR_UNSUPPORTED, "relu2_gate: inner %lld not a multiple of %d",
+                                      (long long)inner, vec);
+    if (rows == 0) return GLSDM_OK;
+    if (!fc || !out) return fail(GLSDM_ERR_ARG, "relu2_gate: null pointer");
+    if ((reinterpret_cast<uintptr_t>(fc) | reinterpret_cast<uintptr_t>(out)) & 15)
+        return fail(GLSDM_ERR_UNSUPPORTED, "relu2_gate: pointers must be 16-byte aligned");
+    const int64_t threads = rows * (inner / vec);
+    if (ceil_div(threads, 256) > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "relu2_gate: too many elements");
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)ceil_div(threads, 256)), block(256);
+    if (dtype == GLSDM_F32)
+        hipLaunchKernelGGL(relu2_gate_kernel<float>, grid, block, 0, st, static_cast<const float *>(fc), rows, inner,
+                           static_cast<float *>(out));
+    else
+        hipLaunchKernelGGL(relu2_gate_kernel<bf16_t>, grid, block, 0, st, static_cast<const bf16_t *>(fc), rows,
+                           inner, static_cast<bf16_t *>(out));
+    return check_launch("relu2_gate_kernel");
+}
 
 extern "C" int glsdm_gate_merge(const void *o, const int64_t *o_strides, const void *gate, const int64_t *gate_strides,
                                 int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t dk, void *out, void *stream)

@@ -1,8 +1,21 @@
 """RMSNorm and the gated squared-ReLU MLP of S/layers/common.py:7-27
-(S/ = projects/gl-sdm/src/gl_sdm/)."""
+(S/ = projects/gl-sdm/src/gl_sdm/).  On the GPU outside autograd the MLP's
+activation ``gate * relu(u)^2`` is one HIP launch (``glsdm_relu2_gate``, the
+same roundings as the tensor ops)."""
 import torch
 from torch import nn
 import torch.nn.functional as F
+
+from .. import _native as N
+
+
+def relu2_gate(h):
+    """``gate * u.relu().square()`` for ``u, gate = h.chunk(2, -1)``, ``h [..., 2*inner]`` contiguous."""
+    inner = h.shape[-1] // 2
+    out = torch.empty((*h.shape[:-1], inner), dtype=h.dtype, device=h.device)
+    N.call("glsdm_relu2_gate", N.ptr(h), N.dtype_code(h), h.numel() // h.shape[-1], inner, N.ptr(out),
+           N.stream(h.device))
+    return out
 
 
 class RMSNorm(nn.Module):
@@ -28,5 +41,11 @@ class MLP(nn.Module):
         self.proj = nn.Linear(inner, dim)
 
     def forward(self, x):
-        u, gate = self.fc(x).chunk(2, -1)
+        h = self.fc(x)
+        inner = h.shape[-1] // 2
+        if (h.is_cuda and h.dtype in (torch.float32, torch.bfloat16) and h.is_contiguous()
+                and inner % (16 // h.element_size()) == 0 and h.data_ptr() % 16 == 0
+                and not (torch.is_grad_enabled() and h.requires_grad)):
+            return self.proj(relu2_gate(h))
+        u, gate = h.chunk(2, -1)
         return self.proj(gate * u.relu().square())

@@ -399,6 +399,16 @@ int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int
 int glsdm_gate_merge(const void *o, const int64_t *o_strides, const void *gate, const int64_t *gate_strides,
                      int32_t dtype, int64_t B, int64_t T, int64_t H, int64_t dk, void *out, void *stream);
 
+/*
+ * The MLP activation: with u, g the halves of each row of fc [rows, 2*inner],
+ * out [rows, inner] = g * relu(u)^2 (the square rounded to dtype, then the
+ * product rounded to dtype).  inner a multiple of 16 bytes' worth of
+ * elements; fc and out 16-byte aligned.
+ * Replaces: u, gate = fc(x).chunk(2, -1); gate * u.relu().square() of
+ * S/layers/common.py:26-27.
+ */
+int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,3 +76,19 @@ def test_gate_merge_matches_tensor_ops(device, dtype, B, H, T, dk):
     torch.testing.assert_close(out, ref, atol=0, rtol=0)
     out2 = gate_merge(o.contiguous(), gate)
     torch.testing.assert_close(out2, ref, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,inner", [(2048, 4096), (37, 64), (1, 8), (300, 128)])
+def test_relu2_gate_matches_tensor_ops(device, dtype, rows, inner):
+    """The MLP activation (S/layers/common.py:26-27) bit for bit, NaN and
+    signed zeros included."""
+    from glsdm.layers.common import relu2_gate
+    g = torch.Generator().manual_seed(rows + inner)
+    h = (torch.randn(rows, 2 * inner, generator=g) * 2).to(dtype)
+    h[0, :4] = torch.tensor([float("nan"), -0.0, 0.0, -3.0]).to(dtype)
+    h = h.to(device)
+    out = relu2_gate(h)
+    u, gate = h.chunk(2, -1)
+    ref = gate * u.relu().square()
+    torch.testing.assert_close(out, ref, atol=0, rtol=0, equal_nan=True)
