@@ -187,9 +187,63 @@ __global__ __launch_bounds__(256) void relu2_gate_kernel(const TX *__restrict__ 
     *reinterpret_cast<typename V::Raw *>(out + r * inner + c) = V::pack(o);
 }
 
+// RMSNorm then a cast (S/layers/common.py:7-17 followed by .to(dtype), as
+// the blocks apply it, S/baselines/block.py and S/layers/global_layer.py):
+// per row x of dim elements, r = rsqrt(mean(x^2) + eps), y = (x * r) * w in
+// fp32 (w the weight rounded to the input dtype) rounded once to the input
+// dtype, then to the output dtype -- the roundings of PyTorch's fused GPU
+// kernel; the mean's summation order differs from it.  One block per row.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict__ x, const float *__restrict__ w,
+                                                            int64_t dim, float eps, TO *__restrict__ out)
+{
+#pragma clang fp contract(off)
+    __shared__ float s_part[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const TI *row = x + (int64_t)blockIdx.x * dim;
+    float ss = 0.0f;
+    for (int64_t i = tid; i < dim; i += 256) {
+        const float v = RowIO<TI>::load(row + i);
+        ss += v * v;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) s_part[wave] = ss;
+    __syncthreads();
+    const float total = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float r = rsqrtf(total / (float)dim + eps);
+    TO *dst = out + (int64_t)blockIdx.x * dim;
+    for (int64_t i = tid; i < dim; i += 256) {
+        const float t = RowIO<TI>::load(row + i) * r;
+        const float y = RowIO<TI>::round(t * RowIO<TI>::round(w[i]));
+        RowIO<TO>::store(dst + i, y);
+    }
+}
+
 }  // namespace glsdm
 
 using namespace glsdm;
+
+extern "C" int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const float *weight, int64_t rows, int64_t dim,
+                                   float eps, void *out, int32_t out_dtype, void *stream)
+{
+    if (rows < 0 || dim < 1) return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad shape");
+    if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype)) return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad dtype");
+    if (rows == 0) return GLSDM_OK;
+    if (rows > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "rms_norm_cast: more than 2^31-1 rows");
+    if (!x || !weight || !out) return fail(GLSDM_ERR_ARG, "rms_norm_cast: null pointer");
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)rows), block(256);
+#define GLSDM_RMS(TI, TO)                                                                                     \
+    hipLaunchKernelGGL((rms_norm_cast_kernel<TI, TO>), grid, block, 0, st, static_cast<const TI *>(x), weight, \
+                       dim, eps, static_cast<TO *>(out))
+    if (x_dtype == GLSDM_F32 && out_dtype == GLSDM_F32) GLSDM_RMS(float, float);
+    else if (x_dtype == GLSDM_F32) GLSDM_RMS(float, bf16_t);
+    else if (out_dtype == GLSDM_F32) GLSDM_RMS(bf16_t, float);
+    else GLSDM_RMS(bf16_t, bf16_t);
+#undef GLSDM_RMS
+    return check_launch("rms_norm_cast_kernel");
+}
 
 extern "C" int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner, void *out, void *stream)
 {

@@ -34,6 +34,6 @@ class Block(nn.Module):
 
     def forward(self, x, cache=None):
         dtype = self.mlp.fc.weight.dtype
-        x = x + self.attn(self.norm1(x).to(dtype), cache=cache)
-        x = x + self.mlp(self.norm2(x).to(dtype))
+        x = x + self.attn(self.norm1.cast(x, dtype), cache=cache)
+        x = x + self.mlp(self.norm2.cast(x, dtype))
         return x, regulariser(x, self.reg_mode), x.new_zeros(())

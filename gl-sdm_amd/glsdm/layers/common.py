@@ -28,6 +28,19 @@ class RMSNorm(nn.Module):
     def forward(self, x):
         return F.rms_norm(x, (x.shape[-1],), self.weight.to(x.dtype), eps=1e-6)
 
+    def cast(self, x, dtype):
+        """``self(x).to(dtype)``; on the GPU outside autograd one HIP launch
+        (``glsdm_rms_norm_cast``) instead of the norm and the cast."""
+        w = self.weight
+        if (x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and dtype in (torch.float32, torch.bfloat16)
+                and w.dtype == torch.float32 and x.is_contiguous()
+                and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))):
+            out = torch.empty(x.shape, dtype=dtype, device=x.device)
+            N.call("glsdm_rms_norm_cast", N.ptr(x), N.dtype_code(x), N.ptr(w), x.numel() // x.shape[-1],
+                   x.shape[-1], 1e-6, N.ptr(out), N.dtype_code(out), N.stream(x.device))
+            return out
+        return self(x).to(dtype)
+
 
 class MLP(nn.Module):
     """``proj(gate * relu(u)^2)`` with ``u, gate = fc(x).chunk(2)``; inner width 4*dim by default."""

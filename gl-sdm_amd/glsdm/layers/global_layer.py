@@ -30,10 +30,10 @@ class GlobalLayer(nn.Module):
         B, T, _ = x.shape
         router = self.attn
         dtype = router.q.weight.dtype
-        scores = router.q(self.norm1(x).to(dtype)).view(B, T, router.heads, -1)
+        scores = router.q(self.norm1.cast(x, dtype)).view(B, T, router.heads, -1)
         readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
         x = x + router.proj(router.read_norm(readings.to(dtype)).flatten(-2))
-        x = x + self.mlp(self.norm2(x).to(dtype))
+        x = x + self.mlp(self.norm2.cast(x, dtype))
         return x, regulariser(x, self.reg_mode), x.new_zeros(())
 
     def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None):

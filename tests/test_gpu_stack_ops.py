@@ -92,3 +92,26 @@ def test_relu2_gate_matches_tensor_ops(device, dtype, rows, inner):
     u, gate = h.chunk(2, -1)
     ref = gate * u.relu().square()
     torch.testing.assert_close(out, ref, atol=0, rtol=0, equal_nan=True)
+
+
+@pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
+                                               (torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,dim", [(2048, 1024), (37, 32), (5, 4096), (64, 100)])
+def test_rms_norm_cast_matches_tensor_ops(device, x_dtype, out_dtype, rows, dim):
+    """RMSNorm (learned weight, eps 1e-6) then a cast, against the module's
+    tensor ops: the mean's summation order differs, so a rare value may round
+    the other way once (one ulp of the rounding dtype)."""
+    from glsdm.layers.common import RMSNorm
+    g = torch.Generator().manual_seed(rows + dim)
+    norm = RMSNorm(dim)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(dim, generator=g) + 0.5)
+    norm = norm.to(device)
+    x = (torch.randn(rows, dim, generator=g) * 3).to(x_dtype).to(device)
+    with torch.no_grad():
+        out = norm.cast(x, out_dtype)
+        ref = norm(x).to(out_dtype)
+    assert out.dtype == out_dtype
+    coarse = torch.bfloat16 in (x_dtype, out_dtype)
+    torch.testing.assert_close(out.float(), ref.float(), atol=1e-6, rtol=2 ** -6 if coarse else 1e-5)
+    assert (out != ref).float().mean().item() < (2e-3 if coarse else 1.0)
