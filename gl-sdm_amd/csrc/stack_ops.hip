@@ -193,8 +193,8 @@ __global__ __launch_bounds__(256) void relu2_gate_kernel(const TX *__restrict__ 
 // fp32 (w the weight rounded to the input dtype) rounded once to the input
 // dtype, then to the output dtype -- the roundings of PyTorch's fused GPU
 // kernel; the mean's summation order differs from it.  One block per row.
-template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict__ x, const float *__restrict__ w,
+template <typename TI, typename TO, typename TW>
+__global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict__ x, const TW *__restrict__ w,
                                                             int64_t dim, float eps, TO *__restrict__ out)
 {
 #pragma clang fp contract(off)
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict
     TO *dst = out + (int64_t)blockIdx.x * dim;
     for (int64_t i = tid; i < dim; i += 256) {
         const float t = RowIO<TI>::load(row + i) * r;
-        const float y = RowIO<TI>::round(t * RowIO<TI>::round(w[i]));
+        const float y = RowIO<TI>::round(t * RowIO<TI>::round(RowIO<TW>::load(w + i)));
         RowIO<TO>::store(dst + i, y);
     }
 }
@@ -224,24 +224,36 @@ __global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict
 
 using namespace glsdm;
 
-extern "C" int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const float *weight, int64_t rows, int64_t dim,
-                                   float eps, void *out, int32_t out_dtype, void *stream)
+template <typename TW>
+static void launch_rms(const void *x, int32_t x_dtype, const void *weight, int64_t rows, int64_t dim, float eps,
+                       void *out, int32_t out_dtype, hipStream_t st)
 {
-    if (rows < 0 || dim < 1) return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad shape");
-    if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype)) return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad dtype");
-    if (rows == 0) return GLSDM_OK;
-    if (rows > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "rms_norm_cast: more than 2^31-1 rows");
-    if (!x || !weight || !out) return fail(GLSDM_ERR_ARG, "rms_norm_cast: null pointer");
-    const hipStream_t st = as_stream(stream);
+    const TW *w = static_cast<const TW *>(weight);
     const dim3 grid((unsigned)rows), block(256);
 #define GLSDM_RMS(TI, TO)                                                                                     \
-    hipLaunchKernelGGL((rms_norm_cast_kernel<TI, TO>), grid, block, 0, st, static_cast<const TI *>(x), weight, \
+    hipLaunchKernelGGL((rms_norm_cast_kernel<TI, TO, TW>), grid, block, 0, st, static_cast<const TI *>(x), w,  \
                        dim, eps, static_cast<TO *>(out))
     if (x_dtype == GLSDM_F32 && out_dtype == GLSDM_F32) GLSDM_RMS(float, float);
     else if (x_dtype == GLSDM_F32) GLSDM_RMS(float, bf16_t);
     else if (out_dtype == GLSDM_F32) GLSDM_RMS(bf16_t, float);
     else GLSDM_RMS(bf16_t, bf16_t);
 #undef GLSDM_RMS
+}
+
+extern "C" int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const void *weight, int32_t w_dtype, int64_t rows,
+                                   int64_t dim, float eps, void *out, int32_t out_dtype, void *stream)
+{
+    if (rows < 0 || dim < 1) return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad shape");
+    if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype) || !dtype_ok(w_dtype))
+        return fail(GLSDM_ERR_ARG, "rms_norm_cast: bad dtype");
+    if (rows == 0) return GLSDM_OK;
+    if (rows > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "rms_norm_cast: more than 2^31-1 rows");
+    if (!x || !weight || !out) return fail(GLSDM_ERR_ARG, "rms_norm_cast: null pointer");
+    const hipStream_t st = as_stream(stream);
+    if (w_dtype == GLSDM_F32)
+        launch_rms<float>(x, x_dtype, weight, rows, dim, eps, out, out_dtype, st);
+    else
+        launch_rms<bf16_t>(x, x_dtype, weight, rows, dim, eps, out, out_dtype, st);
     return check_launch("rms_norm_cast_kernel");
 }
 

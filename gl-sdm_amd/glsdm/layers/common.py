@@ -32,12 +32,13 @@ class RMSNorm(nn.Module):
         """``self(x).to(dtype)``; on the GPU outside autograd one HIP launch
         (``glsdm_rms_norm_cast``) instead of the norm and the cast."""
         w = self.weight
-        if (x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and dtype in (torch.float32, torch.bfloat16)
-                and w.dtype == torch.float32 and x.is_contiguous()
+        kinds = (torch.float32, torch.bfloat16)
+        if (x.is_cuda and x.dtype in kinds and dtype in kinds and w.dtype in kinds and w.is_contiguous()
                 and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))):
+            x = x.contiguous()
             out = torch.empty(x.shape, dtype=dtype, device=x.device)
-            N.call("glsdm_rms_norm_cast", N.ptr(x), N.dtype_code(x), N.ptr(w), x.numel() // x.shape[-1],
-                   x.shape[-1], 1e-6, N.ptr(out), N.dtype_code(out), N.stream(x.device))
+            N.call("glsdm_rms_norm_cast", N.ptr(x), N.dtype_code(x), N.ptr(w), N.dtype_code(w),
+                   x.numel() // x.shape[-1], x.shape[-1], 1e-6, N.ptr(out), N.dtype_code(out), N.stream(x.device))
             return out
         return self(x).to(dtype)
 

@@ -411,13 +411,13 @@ int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner,
 
 /*
  * RMSNorm then a cast: per row of x [rows, dim] (x_dtype), r =
- * rsqrt(mean(x^2) + eps), y = (x*r)*w in fp32 rounded to x_dtype (w, fp32
- * [dim], rounded to x_dtype first), y written as out_dtype to out [rows, dim].
+ * rsqrt(mean(x^2) + eps), y = (x*r)*w in fp32 rounded to x_dtype (w [dim] of
+ * w_dtype, rounded to x_dtype first), y written as out_dtype to out [rows, dim].
  * Replaces: RMSNorm.forward (S/layers/common.py:7-17) followed by .to(dtype)
  * in the blocks (S/baselines/block.py, S/layers/global_layer.py:23-31).
  */
-int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const float *weight, int64_t rows, int64_t dim,
-                        float eps, void *out, int32_t out_dtype, void *stream);
+int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const void *weight, int32_t w_dtype, int64_t rows,
+                        int64_t dim, float eps, void *out, int32_t out_dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -96,8 +96,9 @@ def test_relu2_gate_matches_tensor_ops(device, dtype, rows, inner):
 
 @pytest.mark.parametrize("x_dtype,out_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float32),
                                                (torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("w_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,dim", [(2048, 1024), (37, 32), (5, 4096), (64, 100)])
-def test_rms_norm_cast_matches_tensor_ops(device, x_dtype, out_dtype, rows, dim):
+def test_rms_norm_cast_matches_tensor_ops(device, x_dtype, out_dtype, w_dtype, rows, dim):
     """RMSNorm (learned weight, eps 1e-6) then a cast, against the module's
     tensor ops: the mean's summation order differs, so a rare value may round
     the other way once (one ulp of the rounding dtype)."""
@@ -107,6 +108,7 @@ def test_rms_norm_cast_matches_tensor_ops(device, x_dtype, out_dtype, rows, dim)
     with torch.no_grad():
         norm.weight.copy_(torch.rand(dim, generator=g) + 0.5)
     norm = norm.to(device)
+    norm.weight.data = norm.weight.data.to(w_dtype)          # a bf16 model's norm weight
     x = (torch.randn(rows, dim, generator=g) * 3).to(x_dtype).to(device)
     with torch.no_grad():
         out = norm.cast(x, out_dtype)
