@@ -51,19 +51,25 @@ def gate_merge(o, gate):
 _MASKS = {}
 
 
-def _window_mask(previous, T, window, device):
+def _window_mask(previous, T, window, device, dtype):
     """Query i (position offset + i) may see key j (position offset - previous + j)
     when the key is not later and, with a window, less than ``window`` back.  It
     depends on (previous, T, window) only, not on the offset, so one tensor per
-    shape is kept (prefill chunks and decode steps reuse it)."""
-    key = (previous, T, window, device)
+    shape is kept (prefill chunks and decode steps reuse it), already in the
+    additive form SDPA makes of a boolean mask (0 where allowed, -inf where not,
+    in the query dtype), which saves that conversion at every call."""
+    key = (previous, T, window, device, dtype)
     mask = _MASKS.get(key)
     if mask is None:
-        kpos = torch.arange(-previous, T, device=device)[None, :]
-        qpos = torch.arange(0, T, device=device)[:, None]
-        mask = kpos <= qpos
-        if window is not None:
-            mask = mask & (kpos > qpos - window)
+        # an ordinary tensor even when first built under inference mode, so that
+        # autograd may save it later
+        with torch.inference_mode(False), torch.no_grad():
+            kpos = torch.arange(-previous, T, device=device)[None, :]
+            qpos = torch.arange(0, T, device=device)[:, None]
+            allowed = kpos <= qpos
+            if window is not None:
+                allowed = allowed & (kpos > qpos - window)
+            mask = torch.zeros(allowed.shape, dtype=dtype, device=device).masked_fill_(~allowed, float("-inf"))
         if len(_MASKS) >= 64:
             _MASKS.clear()
         _MASKS[key] = mask
@@ -136,7 +142,7 @@ class Transformer(nn.Module):
         # needs this offset causal mask (SDPA's own causal mask is upper-left aligned)
         mask = None
         if offset or self.window is not None:
-            mask = _window_mask(previous, T, self.window, x.device)
+            mask = _window_mask(previous, T, self.window, x.device, q.dtype)
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
         if fused and out.stride(-1) == 1 and gate.stride(-1) == 1 and not (
                 torch.is_grad_enabled() and (out.requires_grad or gate.requires_grad)):

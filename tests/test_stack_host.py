@@ -138,3 +138,18 @@ def test_kv_cache_decode_equals_full_pass():
             parts.append(layer(x[:, t:t + n], cache))
             t += n
         torch.testing.assert_close(torch.cat(parts, 1), full, atol=1e-6, rtol=1e-5)
+
+
+def test_window_mask_cache():
+    """The cached additive mask: 0 where query i may see key j (not later, less
+    than the window back), -inf elsewhere; built once per shape, and never an
+    inference tensor (autograd may save it after a first inference-mode call)."""
+    from glsdm.layers.attention import _window_mask
+    with torch.inference_mode():
+        m = _window_mask(3, 5, 4, torch.device("cpu"), torch.float32)
+    assert not m.is_inference() and m.shape == (5, 8)
+    kpos = torch.arange(-3, 5)[None, :]
+    qpos = torch.arange(5)[:, None]
+    allowed = (kpos <= qpos) & (kpos > qpos - 4)
+    assert torch.equal(m == 0, allowed) and torch.isinf(m[~allowed]).all()
+    assert _window_mask(3, 5, 4, torch.device("cpu"), torch.float32) is m
