@@ -8,11 +8,28 @@ from .attention import Transformer
 from .common import MLP, RMSNorm
 
 
+_ZEROS = {}
+
+
+def zero(x, dtype=None):
+    """A 0-d zero of ``dtype`` (default ``x.dtype``) on ``x``'s device, one shared
+    tensor per (device, dtype): the regularisers of ``reg_mode == "baseline"`` are
+    identically zero, and a fresh fill per layer and chunk is a launch each.
+    Read-only; built outside inference mode so autograd may use it."""
+    key = (x.device, dtype or x.dtype)
+    z = _ZEROS.get(key)
+    if z is None:
+        with torch.inference_mode(False), torch.no_grad():
+            z = torch.zeros((), dtype=key[1], device=key[0])
+        _ZEROS[key] = z
+    return z
+
+
 def regulariser(x, reg_mode):
     """The stack's representation regulariser; only ``reg_mode == "baseline"``
     (zero, S/layers/regularization.py:67-68) is part of the operator build."""
     del reg_mode
-    return x.new_zeros((), dtype=torch.float32)
+    return zero(x, torch.float32)
 
 
 def check_reg_mode(cfg):
@@ -36,4 +53,4 @@ class Block(nn.Module):
         dtype = self.mlp.fc.weight.dtype
         x = x + self.attn(self.norm1.cast(x, dtype), cache=cache)
         x = x + self.mlp(self.norm2.cast(x, dtype))
-        return x, regulariser(x, self.reg_mode), x.new_zeros(())
+        return x, regulariser(x, self.reg_mode), zero(x)

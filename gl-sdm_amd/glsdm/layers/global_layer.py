@@ -7,7 +7,7 @@ import torch.nn.functional as F
 
 from ..memory import routing
 from ..memory.proposals import layer_proposal
-from .block import check_reg_mode, regulariser
+from .block import check_reg_mode, regulariser, zero
 from .common import MLP, RMSNorm
 from .router import GlobalRouter
 
@@ -34,7 +34,7 @@ class GlobalLayer(nn.Module):
         readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
         x = x + router.proj(router.read_norm(readings.to(dtype)).flatten(-2))
         x = x + self.mlp(self.norm2.cast(x, dtype))
-        return x, regulariser(x, self.reg_mode), x.new_zeros(())
+        return x, regulariser(x, self.reg_mode), zero(x)
 
     def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None):
         """Write proposal of the chunk's tokens against ``snapshot``.

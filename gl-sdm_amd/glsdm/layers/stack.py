@@ -16,7 +16,7 @@ commit exists to avoid.
 import torch
 
 from ..memory import commit, merge
-from .block import Block
+from .block import Block, zero
 from .global_layer import GlobalLayer
 
 
@@ -66,7 +66,8 @@ def forward(model, inputs, cache=None):
                     proposals.append(block.propose(x, snapshot, offset, i, C, layers))
             else:
                 x, r, a = block(x, cache.local.setdefault(i, {}))
-            reg, align = reg + r * (length / T), align + a
+            if r is not zero(r) or a is not zero(a):     # the baseline's are the shared zeros: nothing to add
+                reg, align = reg + r * (length / T), align + a
         cache.tokens += length
         if cache.tokens % C == 0 and writes:
             cache.view = commit(snapshot, merge(snapshot, proposals), donate=in_place)
