@@ -220,9 +220,47 @@ __global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict
     }
 }
 
+// The write gates of a global layer's proposal (S/layers/global_layer.py:48-49):
+// beta = sigmoid(b) = 1 / (1 + exp(-b)) and log_decay = -softplus(d - 4) with
+// softplus(v) = v above 20, else log1p(exp(v)), from the bf16 or fp32 outputs
+// of the beta and decay projections, in fp32.  One thread per (token, head).
+template <typename TX>
+__global__ __launch_bounds__(256) void write_gates_kernel(const TX *__restrict__ b, const TX *__restrict__ d,
+                                                          int64_t n, float *__restrict__ beta,
+                                                          float *__restrict__ log_decay)
+{
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float bv = RowIO<TX>::load(b + i);
+    beta[i] = 1.0f / (1.0f + expf(-bv));
+    const float v = RowIO<TX>::load(d + i) - 4.0f;
+    const float sp = v > 20.0f ? v : log1pf(expf(v));
+    log_decay[i] = -sp;
+}
+
 }  // namespace glsdm
 
 using namespace glsdm;
+
+extern "C" int glsdm_write_gates(const void *beta_in, const void *decay_in, int32_t dtype, int64_t n, float *beta,
+                                 float *log_decay, void *stream)
+{
+    if (n < 0) return fail(GLSDM_ERR_ARG, "write_gates: bad shape");
+    if (!dtype_ok(dtype)) return fail(GLSDM_ERR_ARG, "write_gates: bad dtype");
+    if (n == 0) return GLSDM_OK;
+    if (!beta_in || !decay_in || !beta || !log_decay) return fail(GLSDM_ERR_ARG, "write_gates: null pointer");
+    if (ceil_div(n, 256) > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "write_gates: too many elements");
+    const hipStream_t st = as_stream(stream);
+    const dim3 grid((unsigned)ceil_div(n, 256)), block(256);
+    if (dtype == GLSDM_F32)
+        hipLaunchKernelGGL(write_gates_kernel<float>, grid, block, 0, st, static_cast<const float *>(beta_in),
+                           static_cast<const float *>(decay_in), n, beta, log_decay);
+    else
+        hipLaunchKernelGGL(write_gates_kernel<bf16_t>, grid, block, 0, st, static_cast<const bf16_t *>(beta_in),
+                           static_cast<const bf16_t *>(decay_in), n, beta, log_decay);
+    return check_launch("write_gates_kernel");
+}
 
 template <typename TW>
 static void launch_rms(const void *x, int32_t x_dtype, const void *weight, int64_t rows, int64_t dim, float eps,

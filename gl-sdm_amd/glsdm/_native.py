@@ -42,6 +42,7 @@ SIGNATURES = {
     "glsdm_gate_merge": ([_P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "glsdm_relu2_gate": ([_P, _I32, _I64, _I64, _P, _P], _I32),
     "glsdm_rms_norm_cast": ([_P, _I32, _P, _I32, _I64, _I64, ctypes.c_float, _P, _I32, _P], _I32),
+    "glsdm_write_gates": ([_P, _P, _I32, _I64, _P, _P, _P], _I32),
     "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),
     "glsdm_proposal_error": ([_I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _P], _I32),
     "glsdm_proposal_delta": ([_P, _I32, _I64, _I32, _I64, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _P], _I32),

@@ -5,11 +5,23 @@ import torch
 from torch import nn
 import torch.nn.functional as F
 
+from .. import _native as N
 from ..memory import routing
 from ..memory.proposals import layer_proposal
 from .block import check_reg_mode, regulariser, zero
 from .common import MLP, RMSNorm
 from .router import GlobalRouter
+
+
+def write_gates(b_lin, d_lin):
+    """``(sigmoid(b) [..., 1], -softplus(d - 4) [..., 1])`` in fp32 from the beta and
+    decay projections' outputs, in one HIP launch (``glsdm_write_gates``)."""
+    b_lin, d_lin = b_lin.contiguous(), d_lin.contiguous()
+    beta = torch.empty(b_lin.shape, dtype=torch.float32, device=b_lin.device)
+    log_decay = torch.empty_like(beta)
+    N.call("glsdm_write_gates", N.ptr(b_lin), N.ptr(d_lin), N.dtype_code(b_lin), b_lin.numel(), N.ptr(beta),
+           N.ptr(log_decay), N.stream(b_lin.device))
+    return beta.unsqueeze(-1), log_decay.unsqueeze(-1)
 
 
 class GlobalLayer(nn.Module):
@@ -51,12 +63,17 @@ class GlobalLayer(nn.Module):
         training = torch.is_grad_enabled() and (x.requires_grad or snapshot.values.requires_grad)
         B, T, _ = x.shape
         router = self.attn
-        z = self.norm1(x)
-        scores = router.k(z.to(router.k.weight.dtype)).view(B, T, router.heads, -1)
+        zk = self.norm1.cast(x, router.k.weight.dtype)
+        scores = router.k(zk).view(B, T, router.heads, -1)
         prediction, index, weights = routing.routed_read(self, snapshot.values, scores, router.num_writes, physical)
-        dense = z.to(router.v.weight.dtype)
+        vdt = router.v.weight.dtype
+        dense = zk if vdt == zk.dtype else self.norm1.cast(x, vdt)
         target = router.v(dense).view(B, T, router.heads, router.head_dim)
-        beta = router.beta(dense).float().sigmoid().unsqueeze(-1)
-        log_decay = -F.softplus(router.decay(dense).float() - 4).unsqueeze(-1)
+        b_lin, d_lin = router.beta(dense), router.decay(dense)
+        if training or not b_lin.is_cuda or b_lin.dtype not in (torch.float32, torch.bfloat16):
+            beta = b_lin.float().sigmoid().unsqueeze(-1)
+            log_decay = -F.softplus(d_lin.float() - 4).unsqueeze(-1)
+        else:
+            beta, log_decay = write_gates(b_lin, d_lin)
         return layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
                               chunk_size, num_layers, deferred=not training)

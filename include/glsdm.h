@@ -419,6 +419,16 @@ int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner,
 int glsdm_rms_norm_cast(const void *x, int32_t x_dtype, const void *weight, int32_t w_dtype, int64_t rows,
                         int64_t dim, float eps, void *out, int32_t out_dtype, void *stream);
 
+/*
+ * The write gates of a proposal from the beta and decay projections' outputs
+ * (n values each, dtype): beta = sigmoid(b), log_decay = -softplus(d - 4)
+ * (softplus(v) = v above 20, else log1p(exp(v))), fp32 [n] each.
+ * Replaces: router.beta(dense).float().sigmoid() and
+ * -F.softplus(router.decay(dense).float() - 4) of S/layers/global_layer.py:48-49.
+ */
+int glsdm_write_gates(const void *beta_in, const void *decay_in, int32_t dtype, int64_t n, float *beta,
+                      float *log_decay, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

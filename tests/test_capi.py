@@ -18,7 +18,7 @@ def test_header_declares_the_expected_surface():
                      "glsdm_overlay_commit", "glsdm_overlay_materialise", "glsdm_route_workspace_bytes",
                      "glsdm_score_route", "glsdm_score_route_keys", "glsdm_score_route_workspace_bytes",
                      "glsdm_commit_prepare", "glsdm_commit_apply", "glsdm_qk_norm_rotary", "glsdm_gate_merge", "glsdm_relu2_gate",
-                     "glsdm_rms_norm_cast"):
+                     "glsdm_rms_norm_cast", "glsdm_write_gates"):
         assert required in names
 
 

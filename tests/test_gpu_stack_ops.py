@@ -117,3 +117,23 @@ def test_rms_norm_cast_matches_tensor_ops(device, x_dtype, out_dtype, w_dtype, r
     coarse = torch.bfloat16 in (x_dtype, out_dtype)
     torch.testing.assert_close(out.float(), ref.float(), atol=1e-6, rtol=2 ** -6 if coarse else 1e-5)
     assert (out != ref).float().mean().item() < (2e-3 if coarse else 1.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_write_gates_match_tensor_ops(device, dtype):
+    """The proposal's write gates (S/layers/global_layer.py:48-49): sigmoid of the
+    beta projection and -softplus(decay - 4), over the softplus threshold and
+    the sigmoid's saturation too, within a few fp32 ulp of the tensor ops."""
+    from glsdm.layers.global_layer import write_gates
+    g = torch.Generator().manual_seed(3)
+    b = (torch.randn(4, 512, 16, generator=g) * 6).to(dtype)
+    d = (torch.randn(4, 512, 16, generator=g) * 12).to(dtype)
+    b[0, 0, :4] = torch.tensor([-100.0, 100.0, 0.0, -0.0]).to(dtype)
+    d[0, 0, :4] = torch.tensor([24.0, 23.9, 25.0, -80.0]).to(dtype)
+    b, d = b.to(device), d.to(device)
+    beta, log_decay = write_gates(b, d)
+    ref_beta = b.float().sigmoid().unsqueeze(-1)
+    ref_ld = -torch.nn.functional.softplus(d.float() - 4).unsqueeze(-1)
+    assert beta.shape == ref_beta.shape == log_decay.shape
+    torch.testing.assert_close(beta, ref_beta, atol=1e-7, rtol=4e-7)
+    torch.testing.assert_close(log_decay, ref_ld, atol=1e-7, rtol=4e-7)
