@@ -69,7 +69,11 @@ def _window_mask(previous, T, window, device, dtype):
             allowed = kpos <= qpos
             if window is not None:
                 allowed = allowed & (kpos > qpos - window)
-            mask = torch.zeros(allowed.shape, dtype=dtype, device=device).masked_fill_(~allowed, float("-inf"))
+            # rows padded to a multiple of 16 elements: attention kernels want an aligned
+            # row stride and would otherwise pad a copy of the mask at every call
+            n = allowed.shape[1]
+            store = torch.zeros((T, (n + 15) // 16 * 16), dtype=dtype, device=device)
+            mask = store[:, :n].masked_fill_(~allowed, float("-inf"))
         if len(_MASKS) >= 64:
             _MASKS.clear()
         _MASKS[key] = mask

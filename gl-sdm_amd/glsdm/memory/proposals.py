@@ -18,6 +18,24 @@ from .state import DeferredProposal, WriteProposal
 from .backends import hip
 
 
+_ONES = {}
+
+
+def _ones(shape, device):
+    """A shared read-only fp32 ones tensor per (shape, device): the stack's mass
+    (one per token) is the same for every proposal, and a fill per layer and
+    chunk is a launch each.  Built outside inference mode so autograd may use it."""
+    key = (tuple(shape), device)
+    t = _ONES.get(key)
+    if t is None:
+        with torch.inference_mode(False), torch.no_grad():
+            t = torch.ones(key[0], dtype=torch.float32, device=device)
+        if len(_ONES) >= 64:
+            _ONES.clear()
+        _ONES[key] = t
+    return t
+
+
 def layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
                    chunk_size, num_layers, mass=None, deferred=True):
     """Proposal of the write route ``index``/``weights [B, T, H, k]`` with its routed
@@ -25,7 +43,7 @@ def layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay
     ``beta``/``log_decay [B, T, H, 1]`` (``mass [B, T]``, default ones)."""
     addresses, keys = hip.proposal_keys(snapshot.values, index, offset, chunk_size, num_layers, layer_idx)
     if mass is None:
-        mass = torch.ones(index.shape[:2], dtype=torch.float32, device=index.device)
+        mass = _ones(index.shape[:2], index.device)
     if deferred:
         return DeferredProposal(snapshot.version, addresses, weights, prediction, target, beta, log_decay, mass,
                                 snapshot.lineage, keys)
