@@ -133,3 +133,25 @@ def test_read_and_score_envelopes():
 def test_errors_become_python_exceptions():
     with pytest.raises(ValueError, match="width"):
         N.call("glsdm_route", None, 0, 4, 8, 0, 0, None, None, None, 0, None)
+
+
+def test_stack_ops_reject_bad_arguments_before_launch():
+    """The fused stack entry points check shapes, dtypes, strides and alignment
+    on the host and return a status; nothing is launched on these."""
+    one = ctypes.c_void_p(16)
+    eps = ctypes.c_float(1e-6)
+    qk = lambda B, dk, stride, offset: _rc("glsdm_qk_norm_rotary", one, 1, B, 2, 1, dk, stride, one, offset, one, None)
+    assert qk(1, 12, 24, 0) == N.ERR_ARG                   # dk not a power of two
+    assert qk(1, 512, 512, 0) == N.ERR_ARG                 # dk above 256
+    assert qk(1, 64, 32, 0) == N.ERR_ARG                   # row stride below dk
+    assert qk(1, 64, 64, 1 << 24) == N.ERR_UNSUPPORTED     # positions not exact in fp32
+    assert qk(0, 64, 64, 0) == N.OK                        # empty
+    assert _rc("glsdm_relu2_gate", one, 1, 4, 12, one, None) == N.ERR_UNSUPPORTED                # inner % 8
+    assert _rc("glsdm_relu2_gate", ctypes.c_void_p(18), 1, 4, 16, one, None) == N.ERR_UNSUPPORTED  # alignment
+    assert _rc("glsdm_relu2_gate", one, 3, 4, 16, one, None) == N.ERR_ARG                         # dtype
+    strided = (ctypes.c_int64 * 4)(64, 64, 64, 2)
+    assert _rc("glsdm_gate_merge", one, strided, one, strided, 1, 1, 1, 1, 64, one, None) == N.ERR_UNSUPPORTED
+    assert _rc("glsdm_rms_norm_cast", one, 1, one, 5, 4, 16, eps, one, 1, None) == N.ERR_ARG      # weight dtype
+    assert _rc("glsdm_rms_norm_cast", one, 1, one, 0, 4, 0, eps, one, 1, None) == N.ERR_ARG       # dim 0
+    assert _rc("glsdm_write_gates", one, one, 1, -1, one, one, None) == N.ERR_ARG
+    assert _rc("glsdm_write_gates", None, None, 1, 0, None, None, None) == N.OK                 # empty
