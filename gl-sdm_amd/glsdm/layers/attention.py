@@ -49,6 +49,7 @@ def gate_merge(o, gate):
 
 
 _MASKS = {}
+APPEND_MAX_TOKENS = 16    # calls of at most this many tokens (decode) append to the KV window in place
 
 
 def _window_mask(previous, T, window, device, dtype):
@@ -117,13 +118,46 @@ class Transformer(nn.Module):
         a, b = x.float().chunk(2, -1)
         return torch.cat((a * cos + b * sin, -a * sin + b * cos), -1).to(x.dtype)
 
+    def _append(self, cache, k, v, previous, offset):
+        """Inference KV cache for short calls (decode): the window lives in a buffer
+        with room to append, so a step writes only its own rows instead of
+        re-concatenating the whole window (window - 1 rows per layer and step); when
+        the room runs out
+        the kept rows move to a fresh buffer.  Returns the visible keys and values
+        (the ``previous`` cached rows, then the new ones) as views of the buffer;
+        ``cache["k"]``/``cache["v"]`` stay views of the last window - 1 rows.  The
+        cache has one owner: two continuations of the same cache would append into
+        the same buffer."""
+        B, H, T, dk = k.shape
+        buf_k, buf_v, end = cache.get("kbuf"), cache.get("vbuf"), cache.get("end", 0)
+        tail = cache.get("k")
+        in_buffer = (buf_k is not None and tail is not None and tail.shape[2] == previous and previous <= end
+                     and (previous == 0 or tail.data_ptr() == buf_k[:, :, end - previous:end].data_ptr()))
+        if not in_buffer or end + T > buf_k.shape[2] or buf_k.dtype != k.dtype or buf_k.device != k.device:
+            room = max(512, T)
+            cap = previous + T + room
+            buf_k = torch.empty((B, H, cap, dk), dtype=k.dtype, device=k.device)
+            buf_v = torch.empty((B, H, cap, dk), dtype=v.dtype, device=v.device)
+            if previous:
+                buf_k[:, :, :previous].copy_(cache["k"])
+                buf_v[:, :, :previous].copy_(cache["v"])
+            end = previous
+        buf_k[:, :, end:end + T].copy_(k)
+        buf_v[:, :, end:end + T].copy_(v)
+        start, end = end - previous, end + T
+        n = previous + T
+        keep = n if self.window is None else min(self.window - 1, n)
+        cache.update(k=buf_k[:, :, end - keep:end], v=buf_v[:, :, end - keep:end], tokens=offset + T, kbuf=buf_k,
+                     vbuf=buf_v, end=end)
+        return buf_k[:, :, start:end], buf_v[:, :, start:end]
+
     def forward(self, x, cache=None):
         B, T, D = x.shape
         dk = self.head_dim
         q, gate = self.q(x).view(B, T, self.num_heads, 2 * dk).chunk(2, -1)
         k = self.k(x).view(B, T, self.num_kv_heads, dk)
         v = self.v(x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
-        previous = cache["k"].shape[2] if cache else 0
+        previous = cache["k"].shape[2] if cache and cache.get("k") is not None else 0
         offset = 0 if cache is None else cache.get("tokens", previous)
         fused = (x.is_cuda and dk in (4, 8, 16, 32, 64, 128, 256) and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
                  and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad)))
@@ -134,11 +168,19 @@ class Transformer(nn.Module):
             q = self.rotary(F.rms_norm(q, (dk,)), offset).transpose(1, 2)
             k = self.rotary(F.rms_norm(k, (dk,)), offset).transpose(1, 2)
         if cache is not None:
-            if cache:
-                k, v = torch.cat((cache["k"], k), 2), torch.cat((cache["v"], v), 2)
-            n = k.shape[2]
-            keep = n if self.window is None else min(self.window - 1, n)
-            cache.update(k=k[:, :, n - keep:], v=v[:, :, n - keep:], tokens=offset + T)
+            if T > APPEND_MAX_TOKENS or (torch.is_grad_enabled() and (k.requires_grad or v.requires_grad)):
+                # prefill chunks and autograd: functional concatenation (attention reads
+                # contiguous windows faster, and appending in place would modify tensors
+                # saved for backward)
+                for name in ("kbuf", "vbuf", "end"):
+                    cache.pop(name, None)
+                if cache.get("k") is not None:
+                    k, v = torch.cat((cache["k"], k), 2), torch.cat((cache["v"], v), 2)
+                n = k.shape[2]
+                keep = n if self.window is None else min(self.window - 1, n)
+                cache.update(k=k[:, :, n - keep:], v=v[:, :, n - keep:], tokens=offset + T)
+            else:
+                k, v = self._append(cache, k, v, previous, offset)
         groups = self.num_heads // self.num_kv_heads
         if groups != 1:
             k, v = k.repeat_interleave(groups, 1), v.repeat_interleave(groups, 1)
