@@ -191,7 +191,10 @@ struct RouteSplit {
 };
 
 constexpr int64_t ROUTE_SPLIT_MIN_BLOCKS = 256;   // single-kernel launches below one block per CU split
-constexpr int64_t ROUTE_SPLIT_TARGET_BLOCKS = 1024;
+#ifndef GLSDM_ROUTE_SPLIT_TARGET
+#define GLSDM_ROUTE_SPLIT_TARGET 1024
+#endif
+constexpr int64_t ROUTE_SPLIT_TARGET_BLOCKS = GLSDM_ROUTE_SPLIT_TARGET;
 
 static int route_group(int K) { return K >= 32 ? 8 : 4; }
 
