@@ -39,6 +39,8 @@
 // the reference's stable key sort followed by grouping of equal consecutive
 // addresses whenever its keys keep equal addresses together (keys = addresses,
 // and the stack's addr*(C*L) + pos*L + layer).
+#include <atomic>
+
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -84,13 +86,25 @@ constexpr uint32_t LB_PREFIX = 2u << 30;                // inclusive prefix publ
 constexpr uint32_t LB_VALUE = LB_AGGREGATE - 1;
 constexpr uint32_t LB_SPIN_LIMIT = 1u << 22;            // bounded wait; exceeded only by a bug
 
+// Workspace words after the per-pass tile counters: the sort's error flags
+// (bit 0: a look-back wait gave up, bit 1: a bucket's pieces were
+// inconsistent; either way the segment step writes nothing), the deferred-run
+// count, and the number of entries dropped for an out-of-range address.
+constexpr int CW_ERROR = MAX_PASSES, CW_LONG = MAX_PASSES + 1, CW_DROPPED = MAX_PASSES + 2;
+constexpr int CW_WORDS = MAX_PASSES + 3;
+
+// Polls of an unpublished predecessor before a look-back wait gives up;
+// glsdm_debug_force_lookback_timeout sets it to 0 (give up at once) so a test
+// can drive the error path from the host.
+static std::atomic<uint32_t> g_spin_limit{LB_SPIN_LIMIT};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct CommitWorkspace {
     uint64_t *a, *b, *c;
     uint32_t *ghist;    // [MAX_PASSES][RADIX] global digit counts
     uint32_t *status;   // [passes][tiles][RADIX] look-back words
-    uint32_t *counter;  // [MAX_PASSES] tile-id counters, an error word, the deferred-run count
+    uint32_t *counter;  // [MAX_PASSES] tile-id counters, then the CW_* words
     int64_t tiles, bucket_tiles;
     size_t status_words;
     size_t bytes;
@@ -106,7 +120,7 @@ static CommitWorkspace plan_workspace(void *base, int64_t entries, int passes)
     const size_t words = align256(sizeof(uint64_t) * (size_t)entries);
     const size_t ghist = align256(sizeof(uint32_t) * MAX_PASSES * RADIX);
     const size_t status = align256(sizeof(uint32_t) * w.status_words);
-    const size_t counter = align256(sizeof(uint32_t) * (MAX_PASSES + 2));
+    const size_t counter = align256(sizeof(uint32_t) * CW_WORDS);
     char *p = static_cast<char *>(base);
     w.a = reinterpret_cast<uint64_t *>(p);
     w.b = reinterpret_cast<uint64_t *>(p + words);
@@ -134,7 +148,18 @@ __global__ __launch_bounds__(256) void commit_prep_kernel(uint32_t *__restrict__
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t i = tid; i < status_words; i += stride) status[i] = 0;
     if (tid < MAX_PASSES * RADIX) ghist[tid] = 0;
-    if (tid < MAX_PASSES + 2) counter[tid] = 0;
+    if (tid < CW_WORDS) counter[tid] = 0;
+}
+
+// The commit's status words for the caller: [0] the sort's error flags, [1]
+// the entries dropped for an out-of-range address (no workspace: zeros).
+__global__ __launch_bounds__(64) void commit_status_kernel(const uint32_t *__restrict__ counter,
+                                                           int64_t *__restrict__ out)
+{
+    if (threadIdx.x == 0) {
+        out[0] = counter ? (int64_t)counter[CW_ERROR] : 0;
+        out[1] = counter ? (int64_t)counter[CW_DROPPED] : 0;
+    }
 }
 
 __global__ __launch_bounds__(256) void pack_hist_kernel(const int64_t *__restrict__ addresses, int64_t rows,
@@ -185,7 +210,7 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
                                                                 const uint32_t *__restrict__ ghist,
                                                                 uint32_t *__restrict__ status,
                                                                 uint32_t *__restrict__ counter,
-                                                                uint32_t *__restrict__ error)
+                                                                uint32_t *__restrict__ error, uint32_t spin_limit)
 {
     static_assert(SORT_THREADS >= RADIX && SORT_THREADS % 64 == 0, "one thread per digit");
     __shared__ uint32_t cnt[SORT_WAVES][RADIX];
@@ -265,8 +290,9 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
             uint32_t spins = 0;
             for (;;) {
                 const uint32_t s = __hip_atomic_load(look, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((s & ~LB_VALUE) == 0) {           // predecessor not published yet
-                    if (++spins > LB_SPIN_LIMIT) { atomicOr(error, 1u); break; }
+                // predecessor not published yet (a zero limit never waits: the host-forced failure)
+                if ((s & ~LB_VALUE) == 0 || spin_limit == 0) {
+                    if (spins++ >= spin_limit) { atomicOr(error, 1u); break; }
                     continue;
                 }
                 prefix += s & LB_VALUE;
@@ -375,7 +401,7 @@ __global__ __launch_bounds__(BT_THREADS) void tile_bucket_kernel(const int64_t *
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const bool owner = tid < RADIX;
     const int64_t tile = blockIdx.x;
-    if (tile == 0 && tid < MAX_PASSES + 2) counter[tid] = 0;
+    if (tile == 0 && tid < CW_WORDS) counter[tid] = 0;
     for (int x = tid; x < BT_WAVES * RADIX; x += BT_THREADS) (&cnt[0][0])[x] = 0;
     __syncthreads();
 
@@ -475,7 +501,7 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(const uint64_t 
                                                                       int64_t tiles, int64_t n,
                                                                       uint64_t *__restrict__ scratch,
                                                                       uint64_t *__restrict__ out, int ebits,
-                                                                      int lpasses)
+                                                                      int lpasses, uint32_t *__restrict__ error)
 {
     __shared__ uint64_t s_x[BK_CAP];
     __shared__ uint64_t s_y[BK_CAP];
@@ -497,7 +523,11 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(const uint64_t 
     block_scan(my_cnt, s_scan, &size32);
     block_scan(my_first, s_scan, &start32);
     const int64_t size = size32, start = start32;
-    if (size == 0 || start + size > n) return;              // block-uniform; the second never holds
+    if (start + size > n) {                                 // block-uniform; never holds after step 1
+        if (tid == 0) atomicOr(error, 2u);
+        return;
+    }
+    if (size == 0) return;
     const bool in_lds = size <= BK_CAP;
     // global path: gather into X, then passes X -> Y -> X ..., the last one into out
     uint64_t *X = ((lpasses % 2 == 0) ? out : scratch) + start;
@@ -731,6 +761,15 @@ template <typename TB> struct OverlayRows {
     }
 };
 
+// The segment step's side words in the workspace: where runs that continue
+// past their window are left (a word buffer the sorted words are not in, and
+// its counter), and the sort's status words (CW_ERROR .. CW_DROPPED).
+struct SegAux {
+    int64_t *long_list;
+    uint32_t *long_count;
+    uint32_t *status;
+};
+
 // One wavefront per window of `win` (a power of two <= 64) consecutive sorted
 // positions; lane groups of `lpr` lanes (one bank row each) walk the address
 // runs that start in the window, continuing past its end when a run does.
@@ -739,10 +778,10 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
                                                       const int64_t *__restrict__ keys, const SRC src,
                                                       const uint64_t *__restrict__ sorted, int64_t n, int ebits,
                                                       int nv, int lpr, int win,
-                                                      unsigned long long *__restrict__ unique_out,
-                                                      int64_t *__restrict__ long_list, uint32_t *__restrict__ long_count)
+                                                      unsigned long long *__restrict__ unique_out, SegAux aux)
 {
 #pragma clang fp contract(off)
+    if (aux.status[0] != 0) return;                     // the sort failed: leave every row untouched
     __shared__ uint64_t s_w[4][64];
     __shared__ int s_head[4][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -788,7 +827,10 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
         const int h = s_head[wave][r];
         const uint64_t hw = s_w[wave][h];
         const int64_t row_addr = (int64_t)(hw >> ebits);
-        if (row_addr >= rows) continue;                 // out-of-range entries: dropped
+        if (row_addr >= rows) {                         // out-of-range entries: dropped, and counted
+            if (li == 0) aux.status[CW_DROPPED - CW_ERROR] = (uint32_t)(n - (p0 + h));   // they sort last
+            continue;
+        }
         // run length: positions after the head with the same address.  DEFER
         // (small windows, which long runs cross many of): a run that continues
         // past the window is left to long_run_kernel
@@ -796,7 +838,7 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
         if constexpr (DEFER) {
             while (h + len < win && p0 + h + len < n && (int64_t)(s_w[wave][h + len] >> ebits) == row_addr) ++len;
             if (h + len == win && crosses) {
-                if (li == 0) long_list[atomicAdd(long_count, 1u)] = p0 + h;
+                if (li == 0) aux.long_list[atomicAdd(aux.long_count, 1u)] = p0 + h;
                 continue;
             }
         } else {
@@ -873,15 +915,15 @@ template <typename TB, typename SRC, typename ROWS, int VEC, int CH>
 __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t D, const int64_t *__restrict__ keys,
                                                        const SRC src, const uint64_t *__restrict__ sorted, int64_t n,
                                                        int ebits, int nv, int lpr,
-                                                       const int64_t *__restrict__ long_list,
-                                                       const uint32_t *__restrict__ long_count)
+                                                       const SegAux aux)
 {
 #pragma clang fp contract(off)
+    if (aux.status[0] != 0) return;
     const int lane = threadIdx.x & 63;
     const int ng = 64 / lpr, grp = lane / lpr, li = lane % lpr;
     const uint64_t mine = (lpr >= 64 ? ~0ull : ((1ull << lpr) - 1ull)) << (grp * lpr);
     const uint64_t emask = (1ull << ebits) - 1ull;
-    const int64_t count = *long_count;
+    const int64_t count = *aux.long_count;
     const int64_t groups = (int64_t)gridDim.x * 4 * ng;
     auto key_of = [&](uint64_t word) -> int64_t {
         const int64_t e = (int64_t)(word & emask);
@@ -903,7 +945,7 @@ __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t
     };
     // every lane of a group runs the same iterations (group-uniform control flow)
     for (int64_t i = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * ng + grp; i < count; i += groups) {
-        const int64_t hp = long_list[i];
+        const int64_t hp = aux.long_list[i];
         const int64_t row_addr = (int64_t)(sorted[hp] >> ebits);
         int len = 1;
         for (;;) {
@@ -1005,18 +1047,10 @@ __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t
     }
 }
 
-// Where segment_kernel leaves the runs that continue past their window: a
-// word buffer of the workspace that the sorted words are not in, and a
-// counter that commit_prep_kernel zeroed.
-struct LongRuns {
-    int64_t *list;
-    uint32_t *count;
-};
-
 template <typename TB, int VEC, typename SRC, typename ROWS>
 static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                              const uint64_t *sorted, int64_t n, int ebits, const RowPlan &p,
-                             int64_t *unique_out, const LongRuns &lr, hipStream_t st)
+                             int64_t *unique_out, const SegAux &lr, hipStream_t st)
 {
     // window: 64 positions per wave when that still makes GLSDM_SEG_WAVES waves,
     // shorter for small commits (so they fill the chip), never below one
@@ -1037,13 +1071,13 @@ static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const i
 #define GLSDM_SEG_LAUNCH(C)                                                                                 \
     if (defer) {                                                                                              \
         hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C, true>), grid, block, 0, st, store, rows, D,  \
-                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, lr.list, lr.count);              \
+                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, lr);                             \
         if ((rc = check_launch("segment_kernel"))) return rc;                                                 \
         hipLaunchKernelGGL((long_run_kernel<TB, SRC, ROWS, VEC, C>), lgrid, block, 0, st, store, D, keys, src, \
-                           sorted, n, ebits, p.nv, p.lpr, lr.list, lr.count);                                 \
+                           sorted, n, ebits, p.nv, p.lpr, lr);                                                \
     } else {                                                                                                  \
         hipLaunchKernelGGL((segment_kernel<TB, SRC, ROWS, VEC, C, false>), grid, block, 0, st, store, rows, D, \
-                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, nullptr, nullptr);               \
+                           keys, src, sorted, n, ebits, p.nv, p.lpr, win, u, lr);                             \
     }
     int rc;
     switch (p.ch) {
@@ -1062,7 +1096,7 @@ static int launch_segment_ch(const ROWS &store, int64_t rows, int64_t D, const i
 template <typename TB, typename TD, typename SRC, typename ROWS>
 static int launch_segment_rows(const ROWS &store, uintptr_t row_bits, int64_t rows, int64_t D, const int64_t *keys,
                                const SRC &src, const void *delta_rows, const uint64_t *sorted, int64_t n,
-                               int ebits, int64_t *unique_out, const LongRuns &lr, hipStream_t st)
+                               int ebits, int64_t *unique_out, const SegAux &lr, hipStream_t st)
 {
     constexpr int VEC = 16 / (sizeof(TB) > sizeof(TD) ? sizeof(TB) : sizeof(TD));
     const bool aligned = ((row_bits | reinterpret_cast<uintptr_t>(delta_rows)) & 15) == 0;
@@ -1080,7 +1114,7 @@ static int launch_segment_rows(const ROWS &store, uintptr_t row_bits, int64_t ro
 template <typename TB, typename TD, typename SRC>
 static int launch_segment_t(void *bank, int64_t rows, int64_t D, const int64_t *keys, const SRC &src,
                             const void *delta_rows, const uint64_t *sorted, int64_t n, int ebits,
-                            int64_t *unique_out, const LongRuns &lr, hipStream_t st)
+                            int64_t *unique_out, const SegAux &lr, hipStream_t st)
 {
     return launch_segment_rows<TB, TD>(DenseRows<TB>{static_cast<TB *>(bank), D}, reinterpret_cast<uintptr_t>(bank),
                                        rows, D, keys, src, delta_rows, sorted, n, ebits, unique_out, lr, st);
@@ -1128,23 +1162,23 @@ static int check_commit(const char *what, int64_t rows, int64_t D, int64_t entri
 // Where commit_sort leaves the sorted words and the deferred-run list for
 // (rows, entries): a function of the shape alone, so a later call (the apply
 // step) finds them without state.
-static void sort_result(const CommitWorkspace &ws, int passes, const uint64_t **sorted, LongRuns *long_runs)
+static void sort_result(const CommitWorkspace &ws, int passes, const uint64_t **sorted, SegAux *aux)
 {
 #if GLSDM_BUCKET_SORT
     if (passes >= 3) {
         *sorted = ws.c;
-        *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.a), ws.counter + MAX_PASSES + 1};
+        *aux = SegAux{reinterpret_cast<int64_t *>(ws.a), ws.counter + CW_LONG, ws.counter + CW_ERROR};
         return;
     }
 #endif
     // LSD passes ping-pong a -> b -> a ...; c is free for the deferred runs
     *sorted = passes % 2 == 0 ? ws.a : ws.b;
-    *long_runs = LongRuns{reinterpret_cast<int64_t *>(ws.c), ws.counter + MAX_PASSES + 1};
+    *aux = SegAux{reinterpret_cast<int64_t *>(ws.c), ws.counter + CW_LONG, ws.counter + CW_ERROR};
 }
 
 static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, void *workspace,
                        size_t workspace_bytes, const char *what, const uint64_t **sorted, int *ebits_out,
-                       LongRuns *long_runs, hipStream_t st)
+                       SegAux *long_runs, hipStream_t st)
 {
     const int ebits = entry_bits(entries), abits = address_bits(rows);
     const int passes = pass_count(abits);
@@ -1162,7 +1196,8 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
                            rows, ebits, msd, entries, ws.b, ws.status, ws.bucket_tiles, ws.counter);
         if ((rc = check_launch("tile_bucket_kernel"))) return rc;
         hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.status, ws.bucket_tiles,
-                           entries, ws.a, ws.c, ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS);
+                           entries, ws.a, ws.c, ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS,
+                           ws.counter + CW_ERROR);
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
         sort_result(ws, passes, sorted, long_runs);
         *ebits_out = ebits;
@@ -1182,7 +1217,8 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
     for (int p = 0; p < passes; ++p) {
         hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)ws.tiles), dim3(SORT_THREADS), 0, st, src, dst, entries,
                            ebits + p * RADIX_BITS, ws.ghist + p * RADIX,
-                           ws.status + (size_t)p * ws.tiles * RADIX, ws.counter + p, ws.counter + MAX_PASSES);
+                           ws.status + (size_t)p * ws.tiles * RADIX, ws.counter + p, ws.counter + CW_ERROR,
+                           g_spin_limit.load(std::memory_order_relaxed));
         if ((rc = check_launch("onesweep_kernel"))) return rc;
         uint64_t *t = src; src = dst; dst = t;
     }
@@ -1194,7 +1230,7 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
 
 template <typename TB, typename TD>
 static int segment_stored(void *bank, int64_t rows, int64_t D, const int64_t *keys, const void *deltas,
-                          const uint64_t *sorted, int64_t n, int ebits, int64_t *unique_out, const LongRuns &lr,
+                          const uint64_t *sorted, int64_t n, int ebits, int64_t *unique_out, const SegAux &lr,
                           hipStream_t st)
 {
     const StoredDeltas<TD> src{static_cast<const TD *>(deltas), D};
@@ -1203,7 +1239,7 @@ static int segment_stored(void *bank, int64_t rows, int64_t D, const int64_t *ke
 
 static int commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, const void *deltas,
                         int32_t delta_dtype, const int64_t *keys, int64_t entries, const uint64_t *sorted, int ebits,
-                        int64_t *unique_out, const LongRuns &lr, hipStream_t st)
+                        int64_t *unique_out, const SegAux &lr, hipStream_t st)
 {
     if (bank_dtype == GLSDM_F32 && delta_dtype == GLSDM_F32)
         return segment_stored<float, float>(bank, rows, D, keys, deltas, sorted, entries, ebits, unique_out, lr, st);
@@ -1228,7 +1264,7 @@ extern "C" int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit", &sorted, &ebits, &lr, st)))
         return rc;
     return commit_apply(bank, bank_dtype, rows, D, deltas, delta_dtype, keys, entries, sorted, ebits, unique_out,
@@ -1245,7 +1281,7 @@ extern "C" int glsdm_commit_prepare(int64_t rows, const int64_t *addresses, int6
     if (!addresses) return fail(GLSDM_ERR_ARG, "commit_prepare: null pointer");
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     return commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit_prepare", &sorted, &ebits, &lr,
                        as_stream(stream));
 }
@@ -1266,7 +1302,7 @@ extern "C" int glsdm_commit_apply(void *bank, int32_t bank_dtype, int64_t rows, 
         return fail(GLSDM_ERR_WORKSPACE, "commit_apply: workspace of %zu bytes needed, %zu given", ws.bytes,
                     workspace_bytes);
     const uint64_t *sorted = nullptr;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     sort_result(ws, passes, &sorted, &lr);
     return commit_apply(bank, bank_dtype, rows, D, deltas, delta_dtype, keys, entries, sorted, entry_bits(entries),
                         unique_out, lr, as_stream(stream));
@@ -1293,7 +1329,7 @@ extern "C" int glsdm_commit_proposals(void *bank, int32_t bank_dtype, int64_t ro
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "commit_proposals", &sorted,
                           &ebits, &lr, st)))
         return rc;
@@ -1323,7 +1359,7 @@ extern "C" int glsdm_read_backward_rows(float *grad_bank, int64_t rows, int64_t 
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "read_backward_rows", &sorted,
                           &ebits, &lr, st)))
         return rc;
@@ -1353,7 +1389,7 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
     const hipStream_t st = as_stream(stream);
     const uint64_t *sorted = nullptr;
     int ebits = 0;
-    LongRuns lr{nullptr, nullptr};
+    SegAux lr{nullptr, nullptr, nullptr};
     if ((rc = commit_sort(rows, addresses, entries, workspace, workspace_bytes, "overlay_commit", &sorted, &ebits,
                           &lr, st)))
         return rc;
@@ -1371,4 +1407,30 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
     if (delta_dtype == GLSDM_F32) GLSDM_OVERLAY(bf16_t, float)
     GLSDM_OVERLAY(bf16_t, bf16_t)
 #undef GLSDM_OVERLAY
+}
+
+extern "C" int glsdm_commit_status(const void *workspace, size_t workspace_bytes, int64_t entries, int64_t rows,
+                                   int64_t *status, void *stream)
+{
+    if (!status) return fail(GLSDM_ERR_ARG, "commit_status: null output");
+    if (rows < 1 || entries < 0) return fail(GLSDM_ERR_ARG, "commit_status: bad shape");
+    const uint32_t *counter = nullptr;
+    if (entries > 0) {
+        int rc = check_commit("commit_status", rows, 1, entries);
+        if (rc) return rc;
+        const CommitWorkspace ws = plan_workspace(const_cast<void *>(workspace), entries,
+                                                  pass_count(address_bits(rows)));
+        if (!workspace || workspace_bytes < ws.bytes)
+            return fail(GLSDM_ERR_WORKSPACE, "commit_status: workspace of %zu bytes needed, %zu given", ws.bytes,
+                        workspace_bytes);
+        counter = ws.counter;
+    }
+    hipLaunchKernelGGL(commit_status_kernel, dim3(1), dim3(64), 0, as_stream(stream), counter, status);
+    return check_launch("commit_status_kernel");
+}
+
+extern "C" int glsdm_debug_force_lookback_timeout(int32_t on)
+{
+    g_spin_limit.store(on ? 0u : LB_SPIN_LIMIT, std::memory_order_relaxed);
+    return GLSDM_OK;
 }

@@ -3,6 +3,7 @@
 The library is the only compute path of this package: if it is missing, or no
 HIP device is present, every native call raises instead of falling back.
 """
+import contextlib
 import ctypes
 import os
 import threading
@@ -36,6 +37,8 @@ SIGNATURES = {
     "glsdm_commit": ([_P, _I32, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),
     "glsdm_commit_prepare": ([_I64, _P, _I64, _P, _SZ, _P], _I32),
     "glsdm_commit_apply": ([_P, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),
+    "glsdm_commit_status": ([_P, _SZ, _I64, _I64, _P, _P], _I32),
+    "glsdm_debug_force_lookback_timeout": ([_I32], _I32),
     "glsdm_absolute_addresses": ([_P, _I64, _I64, _I64, _I32, _I64, _P, _P], _I32),
     "glsdm_proposal_keys": ([_P, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),
     "glsdm_qk_norm_rotary": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
@@ -59,6 +62,50 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib = None
+
+# Debug checks, off by default (each costs a host synchronisation per call):
+#   status -- after every commit-family call, read the commit's device status
+#             words (glsdm_commit_status) and raise NativeError if its sort
+#             failed (no bank row was then written);
+#   bounds -- before a read, gather or commit, check every slot / address
+#             against its range and raise IndexError, as the reference's torch
+#             indexing does (flat[index]), instead of the kernels' documented
+#             skipping of out-of-range entries.
+# GLSDM_CHECKS="status,bounds" in the environment turns them on at import.
+_env_checks = {c.strip() for c in os.environ.get("GLSDM_CHECKS", "").split(",") if c.strip()}
+_checks = {"status": "status" in _env_checks, "bounds": "bounds" in _env_checks}
+
+
+def set_checks(status=None, bounds=None):
+    """Turn the debug checks on or off; returns the previous settings."""
+    prev = dict(_checks)
+    if status is not None:
+        _checks["status"] = bool(status)
+    if bounds is not None:
+        _checks["bounds"] = bool(bounds)
+    return prev
+
+
+@contextlib.contextmanager
+def checks(status=None, bounds=None):
+    prev = set_checks(status, bounds)
+    try:
+        yield
+    finally:
+        set_checks(**prev)
+
+
+def checking(name):
+    return _checks[name]
+
+
+def check_range(index, hi, what):
+    """Bounds check (debug): every element of ``index`` in [0, hi), else IndexError."""
+    if _checks["bounds"] and index is not None and index.numel():
+        bad = (index < 0) | (index >= hi)
+        if bool(bad.any()):
+            first = int(index[bad].reshape(-1)[0])
+            raise IndexError(f"{what}: index {first} is out of bounds for size {hi}")
 
 
 class NativeError(RuntimeError):

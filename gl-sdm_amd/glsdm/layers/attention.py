@@ -97,6 +97,9 @@ class Transformer(nn.Module):
         self.k = nn.Linear(dim, self.num_kv_heads * dk)
         self.v = nn.Linear(dim, self.num_kv_heads * dk)
         self.proj = nn.Linear(dim, dim)
+        # decode steps append to a KV window buffer in place (the cache then has one
+        # owner); gl_commit_in_place = False keeps the reference's functional cache
+        self.append_in_place = bool(cfg.get("gl_commit_in_place", True))
         # rotary frequencies 1024^-u, u in [0, 1], on the first quarter of each
         # half of a head; the second quarter keeps angle 0
         rising = torch.pow(torch.tensor(1 / 1024), torch.linspace(0, 1, dk // 4))
@@ -168,10 +171,12 @@ class Transformer(nn.Module):
             q = self.rotary(F.rms_norm(q, (dk,)), offset).transpose(1, 2)
             k = self.rotary(F.rms_norm(k, (dk,)), offset).transpose(1, 2)
         if cache is not None:
-            if T > APPEND_MAX_TOKENS or (torch.is_grad_enabled() and (k.requires_grad or v.requires_grad)):
-                # prefill chunks and autograd: functional concatenation (attention reads
-                # contiguous windows faster, and appending in place would modify tensors
-                # saved for backward)
+            if (T > APPEND_MAX_TOKENS or not self.append_in_place
+                    or (torch.is_grad_enabled() and (k.requires_grad or v.requires_grad))):
+                # prefill chunks, functional caches and autograd: concatenation (attention
+                # reads contiguous windows faster, a functional cache may be continued
+                # more than once, and appending in place would modify tensors saved for
+                # backward)
                 for name in ("kbuf", "vbuf", "end"):
                     cache.pop(name, None)
                 if cache.get("k") is not None:

@@ -38,6 +38,27 @@ def require_cuda(*tensors):
     return N.require_device(*tensors)
 
 
+def after_commit(name, workspace, entries, rows, device):
+    """The debug status check of a commit-family call (``_native.set_checks``):
+    raise if the commit's sort failed, in which case it wrote no bank row."""
+    if not N.checking("status") or entries == 0:
+        return
+    st = torch.empty(2, dtype=torch.int64, device=device)
+    N.call("glsdm_commit_status", N.ptr(workspace), workspace.numel(), entries, rows, N.ptr(st), N.stream(device))
+    err = int(st[0])
+    if err:
+        raise N.NativeError(f"{name}: the commit's sort failed (flags {err}); no bank row was written")
+
+
+def commit_status(workspace, entries, rows):
+    """``(error flags, dropped entries)`` of the last commit-family call made with
+    ``workspace`` for ``entries`` entries into ``rows`` rows (synchronises)."""
+    device = require_cuda(workspace)
+    st = torch.empty(2, dtype=torch.int64, device=device)
+    N.call("glsdm_commit_status", N.ptr(workspace), workspace.numel(), entries, rows, N.ptr(st), N.stream(device))
+    return tuple(int(x) for x in st.cpu())
+
+
 def _no_grad(*tensors):
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
         raise NotImplementedError("the HIP memory operator is forward-only; run it under torch.no_grad()")
@@ -128,6 +149,7 @@ def _read(values, index, weights, out_dtype):
     if index.dtype != torch.int64 or weights.dtype != torch.float32:
         raise ValueError("snapshot_read needs int64 index and fp32 weights")
     T, width = index.shape[1], index.shape[3]
+    N.check_range(index, S, "snapshot_read")
     out = torch.empty((B, T, H, D), dtype=out_dtype, device=device)
     N.call("glsdm_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, width, N.ptr(index),
            N.ptr(weights), N.ptr(out), N.dtype_code(out), N.stream(device))
@@ -159,11 +181,13 @@ def read_backward_rows(grad_bank, addresses, weights, grad_out, workspace=None):
         raise ValueError("read_backward_rows needs weights [E], grad_out [R, D] with E a multiple of R")
     width = E // R
     rows = grad_bank.numel() // D
+    N.check_range(addresses, rows, "read_backward_rows")
     need = commit_workspace_bytes(E, rows)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=device)
     N.call("glsdm_read_backward_rows", N.ptr(grad_bank), rows, D, N.ptr(addresses), E, width, N.ptr(weights),
            N.ptr(grad_out), N.ptr(workspace), workspace.numel(), N.stream(device))
+    after_commit("read_backward_rows", workspace, E, rows, device)
     return grad_bank
 
 
@@ -349,6 +373,7 @@ def absolute_addresses(values, index):
     B, H, S, _ = values.shape
     if index.ndim != 4 or index.dtype != torch.int64 or index.shape[0] != B or index.shape[2] != H:
         raise ValueError("absolute_addresses needs a [B, T, H, width] int64 index")
+    N.check_range(index, S, "absolute_addresses")
     out = torch.empty_like(index)
     N.call("glsdm_absolute_addresses", N.ptr(index), B, index.shape[1], H, index.shape[3], S, N.ptr(out),
            N.stream(device))
@@ -361,6 +386,7 @@ def proposal_keys(values, index, offset, chunk_size, num_layers, layer_idx):
     B, H, S, _ = values.shape
     if index.ndim != 4 or index.dtype != torch.int64 or index.shape[0] != B or index.shape[2] != H:
         raise ValueError("proposal_keys needs a [B, T, H, width] int64 index")
+    N.check_range(index, S, "proposal_keys")
     addresses = torch.empty_like(index)
     keys = torch.empty_like(index)
     N.call("glsdm_proposal_keys", N.ptr(index), B, index.shape[1], H, index.shape[3], S, offset, chunk_size,
@@ -370,6 +396,7 @@ def proposal_keys(values, index, offset, chunk_size, num_layers, layer_idx):
 
 def _gather(values, addr, shape):
     D = values.shape[-1]
+    N.check_range(addr, values.numel() // D, "gather_rows")
     out = torch.empty((*shape, D), dtype=values.dtype, device=values.device)
     N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), values.numel() // D, D, N.ptr(addr),
            addr.numel(), N.ptr(out), N.stream(values.device))
@@ -412,6 +439,7 @@ def gather_flat(values, addresses):
     if addresses.dtype != torch.int64:
         raise ValueError("gather_flat needs int64 addresses")
     D = values.shape[-1]
+    N.check_range(addresses, values.numel() // D, "gather_rows")
     out = torch.empty((*addresses.shape, D), dtype=values.dtype, device=device)
     N.call("glsdm_gather_rows", N.ptr(values), N.dtype_code(values), values.numel() // D, D, N.ptr(addresses),
            addresses.numel(), N.ptr(out), N.stream(device))
@@ -433,16 +461,18 @@ def _commit(memory, indices, deltas, keys, donate, workspace, unique):
     deltas = deltas.reshape(E, D) if deltas.numel() == E * D else None
     if deltas is None or (keys is not None and keys.numel() != E):
         raise ValueError("commit needs deltas [E, D] and keys [E] matching the addresses")
+    rows = memory.numel() // D
+    N.check_range(indices, rows, "commit")
     out = memory if donate else memory.clone()
     if E == 0:
         return out
-    rows = memory.numel() // D
     need = commit_workspace_bytes(E, rows)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=device)
     N.call("glsdm_commit", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(deltas),
            N.dtype_code(deltas), N.ptr(keys), E, N.ptr(workspace), workspace.numel(), N.ptr(unique),
            N.stream(device))
+    after_commit("commit", workspace, E, rows, device)
     return out
 
 
@@ -563,15 +593,17 @@ def commit_proposals(memory, indices, keys, weights, error, decay, mass, donate=
                          "matching the addresses [..., H, k]")
     if error.dtype != torch.float32 or decay.dtype != torch.float32 or mass.dtype != torch.float32:
         raise ValueError("commit_proposals needs fp32 error, decay and mass")
+    rows = memory.numel() // D
+    N.check_range(indices, rows, "commit_proposals")
     out = memory if donate else memory.clone()
     E = indices.numel()
     if E == 0:
         return out
-    rows = memory.numel() // D
     need = commit_workspace_bytes(E, rows)
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(need, dtype=torch.uint8, device=device)
     N.call("glsdm_commit_proposals", N.ptr(out), N.dtype_code(out), rows, D, N.ptr(indices), N.ptr(keys), E, k,
            N.ptr(weights), N.ptr(error), N.ptr(decay), N.ptr(mass), H, N.ptr(workspace), workspace.numel(),
            N.ptr(unique), N.stream(device))
+    after_commit("commit_proposals", workspace, E, rows, device)
     return out

@@ -76,6 +76,7 @@ class OverlayView:
         if index.ndim != 4 or index.shape[0] != B or index.shape[2] != H or weights.shape != index.shape:
             raise ValueError("overlay read needs [B, T, H, width] int64 index and fp32 weights")
         T, width = index.shape[1], index.shape[3]
+        N.check_range(index, S, "overlay read")
         out = torch.empty((B, T, H, D), dtype=out_dtype, device=index.device)
         N.call("glsdm_overlay_read", N.ptr(self.base), N.dtype_code(self.base), N.ptr(self.map), N.ptr(self.pool),
                B, H, S, D, T, width, N.ptr(index), N.ptr(weights), N.ptr(out), N.dtype_code(out),
@@ -95,6 +96,7 @@ class OverlayView:
         E = addresses.numel()
         if addresses.dtype != torch.int64 or deltas.numel() != E * D or (keys is not None and keys.numel() != E):
             raise ValueError("overlay commit needs int64 addresses [E], deltas [E, D] and keys [E]")
+        N.check_range(addresses, B * H * S, "overlay commit")
         if E:
             self.reserve(E)
             need = hip.commit_workspace_bytes(E, B * H * S)
@@ -105,6 +107,7 @@ class OverlayView:
                    N.ptr(self.pool), self.pool.shape[0], self.next, N.ptr(addresses.contiguous()),
                    N.ptr(deltas), N.dtype_code(deltas), N.ptr(None if keys is None else keys.contiguous()), E,
                    N.ptr(workspace), workspace.numel(), N.ptr(unique), N.stream(deltas.device))
+            hip.after_commit("overlay commit", workspace, E, B * H * S, deltas.device)
             self.next += E
         self.version += 1
         return self

@@ -15,7 +15,9 @@
  *   - Bank / value rows are row-major [rows, D] of dtype GLSDM_F32 or
  *     GLSDM_BF16.  Index tensors are int64, weights and scores fp32.
  *   - Out-of-range slots or addresses never fault: such route entries
- *     contribute nothing to a read and such commit entries are dropped.
+ *     contribute nothing to a read and such commit entries are dropped (and
+ *     counted: glsdm_commit_status).  The reference's torch indexing raises on
+ *     them instead; a caller that wants that checks ranges or the count.
  */
 #ifndef GLSDM_H
 #define GLSDM_H
@@ -210,6 +212,33 @@ int glsdm_commit_prepare(int64_t rows, const int64_t *addresses, int64_t entries
 int glsdm_commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, const void *deltas,
                        int32_t delta_dtype, const int64_t *keys, int64_t entries, void *workspace,
                        size_t workspace_bytes, int64_t *unique_out, void *stream);
+
+/*
+ * Status of the last commit-family call (glsdm_commit, glsdm_commit_apply,
+ * glsdm_commit_proposals, glsdm_read_backward_rows, glsdm_overlay_commit) made
+ * with this workspace and these (entries, rows), written to status (int64[2],
+ * device memory) on the stream after it, without a host synchronisation:
+ *   status[0]: the sort's error flags -- 0, or bit 0 (a bounded look-back wait
+ *              gave up) / bit 1 (inconsistent bucket pieces); when non-zero the
+ *              call wrote no bank row;
+ *   status[1]: the number of entries dropped for an address outside [0, rows).
+ * entries == 0 reports zeros (no workspace needed).
+ * No counterpart in the reference: its sort cannot fail and its torch indexing
+ * raises on an out-of-range address (flat[unique] and index_copy of
+ * S/memory/transactions.py:96); a caller that wants that behaviour raises on
+ * status[1] != 0, or checks the addresses first.
+ */
+int glsdm_commit_status(const void *workspace, size_t workspace_bytes, int64_t entries, int64_t rows,
+                        int64_t *status, void *stream);
+
+/*
+ * Test hook: on != 0 makes every look-back wait of the commit sort give up at
+ * once (commits into fewer than 65536 rows, whose sort uses look-back passes),
+ * so that a test can drive the failure path from the host and check that it
+ * leaves the bank untouched and is reported by glsdm_commit_status; 0 restores
+ * the normal bounded wait.  Process-wide.  No counterpart in the reference.
+ */
+int glsdm_debug_force_lookback_timeout(int32_t on);
 
 /*
  * Absolute addresses (b*H + h)*S + index[b,t,h,j] for index [B,T,H,width].

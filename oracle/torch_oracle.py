@@ -19,6 +19,11 @@ function               reference (``S/`` = ``projects/gl-sdm/src/gl_sdm/``)
 ``commit_dense``       ``S/memory/transactions.py:85-88`` (reference=True branch)
 ``proposal_delta``     ``S/runtime/dense.py:11-14``
 ``proposal_error``     ``S/runtime/dense.py:13`` (the error row alone)
+``token_addresses``    ``S/memory/transactions.py:13-16``
+``token_read``         ``S/memory/transactions.py:19-25,28-35`` (torch branch)
+``token_propose``      ``S/memory/transactions.py:38-59`` (torch branch)
+``score``              ``S/layers/global_layer.py:26,42`` in its per-head
+                       sub-key form (``q @ K^T``, fp32 sequential sums)
 =====================  ==========================================================
 
 Pinning (see ``tests/test_oracle.py``): known answers copied as data from the
@@ -147,3 +152,60 @@ def proposal_delta(rows, weights, prediction, target, beta, log_decay, mass, dec
     g = log_decay.exp() if decay is None else decay
     err = proposal_error(prediction, target, beta, g)
     return mass[..., None, None, None] * ((g[..., None] - 1) * rows + weights[..., None] * err[..., None, :])
+
+
+def token_addresses(values, requests, indices):
+    """Absolute rows ``(request*H + h)*S + index`` of the token-clock API
+    (transactions.py:13-16): ``requests [A]`` (any subset, any order),
+    ``indices [A, H, K]`` against ``values [B, H, S, D]``."""
+    heads, slots = values.shape[1:3]
+    part = requests[:, None, None] * heads + torch.arange(heads, device=indices.device)[None, :, None]
+    return part * slots + indices
+
+
+def _token_rows(values, requests, indices, dense):
+    flat = values.flatten(0, 2)
+    index = token_addresses(values, requests, indices)
+    if dense:
+        return F.one_hot(index.long(), flat.shape[0]).float() @ flat
+    return flat[index]
+
+
+def token_read(values, requests, indices, weights, dense=False):
+    """Token-clock snapshot read ``sum_k w_k * row_k`` -> ``[A, H, D]``
+    (transactions.py:28-35, torch branch; ``dense`` is its reference=True branch)."""
+    rows = _token_rows(values, requests, indices, dense)
+    return (rows * weights.float().unsqueeze(-1)).sum(-2)
+
+
+def token_propose(values, requests, indices, weights, targets, beta, log_decay, mass, dense=False):
+    """Token-clock write proposal (transactions.py:38-59, torch branch).
+
+    Unlike ``proposal_delta`` (dense.py:11-14, the stack's form) the prediction
+    is recomputed from the decayed rows, and the delta is formed as
+    ``decayed - rows + w * error``.  Returns ``(addresses [A*H*K] int64,
+    deltas [A*H*K, D] fp32)``: the fields of the reference's WriteProposal.
+    ``beta``/``log_decay`` are ``[A, H, 1]``, ``mass`` is ``[A]``.
+    """
+    rows = _token_rows(values, requests, indices, dense)
+    decay = log_decay.float().exp().unsqueeze(-1)
+    decayed = rows * decay
+    retrieved = (decayed * weights.float().unsqueeze(-1)).sum(-2)
+    error = beta.float() * (targets.float() - retrieved)
+    delta = decayed - rows + weights.float().unsqueeze(-1) * error.unsqueeze(-2)
+    delta = delta * mass.float()[:, None, None, None]
+    return token_addresses(values, requests, indices).flatten(), delta.flatten(0, 2)
+
+
+def score(queries, subkeys):
+    """Factor scores ``[B, T, H, L]`` fp32 of queries ``[B, T, H, dk]`` against
+    per-head sub-keys ``[H, L, dk]``: ``sum_e q[e] * k[e]`` with e ascending,
+    every product and partial sum rounded to fp32 (the C oracle's loop, as
+    a sequence of torch fp32 ops; global_layer.py:26,42 computes these scores
+    with the router.q/k Linear)."""
+    q = queries.float()
+    k = subkeys.float()
+    acc = torch.zeros(*q.shape[:-1], k.shape[1], dtype=torch.float32)
+    for e in range(q.shape[-1]):
+        acc = acc + q[..., e, None] * k[None, None, :, :, e]
+    return acc

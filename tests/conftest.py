@@ -24,3 +24,18 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     return torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _commit_status_checks(request):
+    """GPU tests run with the commit status check on: every commit-family call
+    reads its device status words and raises if the sort failed."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    from glsdm import _native
+    prev = _native.set_checks(status=True)
+    try:
+        yield
+    finally:
+        _native.set_checks(**prev)

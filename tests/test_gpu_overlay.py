@@ -7,6 +7,7 @@ import torch
 
 from glsdm.memory import OverlayView
 from glsdm.memory.backends import hip
+from oracle import torch_oracle
 from _util import gen
 
 pytestmark = pytest.mark.gpu
@@ -27,23 +28,32 @@ def test_overlay_matches_dense_over_commits(device, dtype, keyed):
     dense = base.unsqueeze(0).expand(B, -1, -1, -1).contiguous()
     ov = OverlayView.from_base(base, B, capacity=64)            # small: forces growth
     base_before = base.cpu()
+    ref_bank = base.cpu().float().unsqueeze(0).expand(B, -1, -1, -1).reshape(-1, D)   # oracle's bank, fp32
     touched = set()
     for step in range(4):
         idx, w = _routes(g, B, T, H, S, width)
+        ref_read = torch_oracle.read(ref_bank.view(B, H, S, D), idx, w)
         idx, w = idx.to(device), w.to(device)
-        assert torch.equal(ov.read(idx, w), hip.snapshot_read(dense, idx, w))
+        got = ov.read(idx, w)
+        assert torch.equal(got, hip.snapshot_read(dense, idx, w))
+        tol = dict(atol=1e-6, rtol=1e-5) if dtype == torch.float32 else dict(atol=1e-5, rtol=2e-2)
+        torch.testing.assert_close(got.cpu(), ref_read, **tol)
         E = 700
         addr = torch.randint(0, B * H * S // 4, (E,), generator=g)        # collisions
         addr[::97] = B * H * S + 5                                         # dropped
         delta = (torch.randn(E, D, generator=g) * 0.01).to(dtype)
         keys = addr * (E + 1) + torch.randperm(E, generator=g) if keyed else None
         touched.update(a for a in addr.tolist() if a < B * H * S)
+        ref = torch_oracle.commit(ref_bank, addr[addr < B * H * S], delta[addr < B * H * S].float(),
+                                  None if keys is None else keys[addr < B * H * S])
+        ref_bank = ref if dtype == torch.float32 else ref.bfloat16().float()   # bf16: one rounding per commit
         addr, delta = addr.to(device), delta.to(device)
         keys = None if keys is None else keys.to(device)
         dense = hip.commit(dense, addr, delta, keys)
         ov.commit(addr, delta, keys)
         assert ov.version == step + 1
         assert torch.equal(ov.materialise(), dense)
+        assert torch.equal(ov.materialise().cpu().float().reshape(-1, D), ref_bank)
     assert ov.mapped_rows() == len(touched)                                # one pool row per touched row
     assert ov.pool.shape[0] >= ov.pool_rows() == 4 * 700 > 64              # reserved per commit; the pool grew
     assert torch.equal(base.cpu(), base_before)                            # the base is never written
@@ -76,3 +86,8 @@ def test_overlay_routed_read(device):
     dense = base.unsqueeze(0).expand(B, -1, -1, -1).contiguous()
     ref, ridx, rw = hip.routed_snapshot_read(dense, scores, width)
     assert torch.equal(idx, ridx) and torch.equal(w, rw) and torch.equal(out, ref)
+    # against the oracle on the materialised bank (routing.py:10-28)
+    o_out, o_idx, o_w = torch_oracle.routed_read(ov.materialise().cpu(), scores.cpu(), width)
+    assert torch.equal(idx.cpu(), o_idx)
+    torch.testing.assert_close(w.cpu(), o_w, atol=2e-7, rtol=2e-6)
+    torch.testing.assert_close(out.cpu(), o_out, atol=1e-6, rtol=1e-5)

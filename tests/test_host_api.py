@@ -105,3 +105,17 @@ def test_route_size_validation():
     with pytest.raises(ValueError):
         hip._square_root(15)
     assert hip._square_root(65536) == 256
+
+
+def test_bounds_check_helper():
+    """The debug bounds check raises IndexError (as torch indexing does) only when on."""
+    from glsdm import _native as N
+    idx = torch.tensor([0, 3, 7])
+    N.check_range(idx, 7, "x")                              # off by default: no check
+    with N.checks(bounds=True):
+        N.check_range(idx, 8, "x")
+        with pytest.raises(IndexError, match="index 7 is out of bounds for size 7"):
+            N.check_range(idx, 7, "x")
+        with pytest.raises(IndexError):
+            N.check_range(torch.tensor([-1]), 7, "x")
+    assert not N.checking("bounds")

@@ -235,3 +235,149 @@ def test_proposal_delta_rule_invariants():
     torch.testing.assert_close(new, ld.exp()[..., None] * rows, atol=1e-6, rtol=1e-5)
     zero = torch_oracle.proposal_delta(rows, w, pred, tgt, beta, ld, torch.zeros_like(mass))
     assert zero.abs().max().item() == 0.0
+
+
+# ---------------------------------------------------------------- scoring
+
+def _score_operands(seed, B=2, T=5, H=3, L=12, dk=64):
+    g = gen(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, dk, generator=g), dim=-1).bfloat16().float()
+    k = torch.nn.functional.normalize(torch.randn(H, L, dk, generator=g), dim=-1).bfloat16().float()
+    return q, k
+
+
+def _score_f64(q, k):
+    return torch.einsum("bthe,hce->bthc", q.double(), k.double())
+
+
+def test_score_float64_closed_form_and_restatements_agree():
+    """oracle_score (C) and torch_oracle.score: bitwise equal to each other
+    (scalar C loop vs a sequence of torch fp32 ops), within fp32 rounding of the
+    float64 contraction, and every element equal to a numpy float32 scalar loop
+    (one rounding per product and per add, e ascending)."""
+    np = pytest.importorskip("numpy")
+    q, k = _score_operands(21)
+    a = c_oracle.score(q, k)
+    b = torch_oracle.score(q, k)
+    assert torch.equal(a, b)
+    torch.testing.assert_close(a.double(), _score_f64(q, k), atol=1e-5, rtol=1e-5)
+    f = np.float32
+    qn, kn = q.numpy(), k.numpy()
+    for (bb, t, h, c) in [(0, 0, 0, 0), (1, 4, 2, 11), (0, 3, 1, 7), (1, 2, 0, 5)]:
+        s = f(0)
+        for e in range(q.shape[-1]):
+            s = f(s + f(qn[bb, t, h, e] * kn[h, c, e]))
+        assert np.float32(a[bb, t, h, c].item()) == s
+
+
+def test_score_planted_mistakes_fail_the_pin():
+    """Plausible slips -- another head's sub-keys, a transposed (factor, dim)
+    operand, a dropped term -- each fail the float64 closed-form check."""
+    q, k = _score_operands(22, L=64, dk=64)
+    exact = _score_f64(q, k)
+
+    def close(x):
+        return torch.allclose(x.double(), exact, atol=1e-5, rtol=1e-5)
+
+    assert close(c_oracle.score(q, k))
+    assert not close(c_oracle.score(q, k.roll(1, 0)))                  # wrong head
+    assert not close(c_oracle.score(q, k.transpose(1, 2).contiguous()))  # transposed operand
+    dropped = q.clone()
+    dropped[..., -1] = 0
+    assert not close(c_oracle.score(dropped, k))                        # dropped term
+
+
+# ---------------------------------------------------------------- token clock
+
+def _token_operands(seed, B=3, H=2, S=67, D=37, K=3, A=2):
+    g = gen(seed)
+    values = torch.randn(B, H, S, D, generator=g)
+    requests = torch.tensor([2, 0])[:A]                     # ACT subset, noncanonical order
+    idx = torch.stack([torch.randperm(S, generator=g)[:K] for _ in range(A * H)]).view(A, H, K)
+    w = torch.randn(A, H, K, generator=g).softmax(-1)
+    tgt = torch.randn(A, H, D, generator=g)
+    beta = torch.rand(A, H, 1, generator=g)
+    ld = -torch.rand(A, H, 1, generator=g)
+    mass = torch.rand(A, generator=g)
+    return values, requests, idx, w, tgt, beta, ld, mass
+
+
+def test_token_addresses_closed_form():
+    values, requests, idx, *_ = _token_operands(30)
+    B, H, S, _ = values.shape
+    addr = torch_oracle.token_addresses(values, requests, idx)
+    for a in range(idx.shape[0]):
+        for h in range(H):
+            for j in range(idx.shape[2]):
+                assert addr[a, h, j].item() == (requests[a].item() * H + h) * S + idx[a, h, j].item()
+
+
+def test_token_read_closed_form_and_dense():
+    values, requests, idx, w, *_ = _token_operands(31)
+    a = torch_oracle.token_read(values, requests, idx, w)
+    b = torch_oracle.token_read(values, requests, idx, w, dense=True)
+    rows = values.double()[requests[:, None, None], torch.arange(values.shape[1])[None, :, None], idx]
+    exact = (rows * w.double()[..., None]).sum(-2)
+    for x in (a, b):
+        torch.testing.assert_close(x.double(), exact, atol=5e-7, rtol=2e-6)
+
+
+def test_token_propose_closed_form():
+    values, requests, idx, w, tgt, beta, ld, mass = _token_operands(32)
+    addr, delta = torch_oracle.token_propose(values, requests, idx, w, tgt, beta, ld, mass)
+    rows = values.double()[requests[:, None, None], torch.arange(values.shape[1])[None, :, None], idx]
+    g = ld.double().exp()[..., None]
+    pred = (rows * g * w.double()[..., None]).sum(-2)
+    err = beta.double() * (tgt.double() - pred)
+    exact = mass.double()[:, None, None, None] * (g * rows - rows + w.double()[..., None] * err[..., None, :])
+    torch.testing.assert_close(delta.double(), exact.flatten(0, 2), atol=5e-7, rtol=2e-6)
+    assert torch.equal(addr, torch_oracle.token_addresses(values, requests, idx).flatten())
+    _, dense = torch_oracle.token_propose(values, requests, idx, w, tgt, beta, ld, mass, dense=True)
+    torch.testing.assert_close(dense, delta, atol=5e-7, rtol=2e-6)
+
+
+def test_token_propose_elementwise_rounding():
+    """With two routes per head the prediction's sum is one fp32 add, so every
+    delta element is the reference's sequence of fp32 roundings exactly."""
+    np = pytest.importorskip("numpy")
+    values, requests, idx, w, tgt, beta, ld, mass = _token_operands(33, D=4, K=2)
+    _, delta = torch_oracle.token_propose(values, requests, idx, w, tgt, beta, ld, mass)
+    delta = delta.view(2, 2, 2, 4)
+    f = np.float32
+    H = values.shape[1]
+    for a in range(2):
+        for h in range(H):
+            gg = f(ld[a, h, 0].exp().item())
+            rows = [[f(values[requests[a], h, idx[a, h, j], d].item()) for d in range(4)] for j in range(2)]
+            ww = [f(w[a, h, j].item()) for j in range(2)]
+            dec = [[f(r * gg) for r in row] for row in rows]
+            for d in range(4):
+                pred = f(f(dec[0][d] * ww[0]) + f(dec[1][d] * ww[1]))
+                err = f(f(beta[a, h, 0].item()) * f(f(tgt[a, h, d].item()) - pred))
+                for j in range(2):
+                    x = f(f(f(dec[j][d] - rows[j][d]) + f(ww[j] * err)) * f(mass[a].item()))
+                    assert np.float32(delta[a, h, j, d].item()) == x
+
+
+def test_token_propose_rule_invariants_and_stack_form():
+    """Fixed points of the token-clock delta rule -- one full-weight write with
+    beta = 1 moves the row to the target whatever the decay; beta = 0 only
+    decays it; mass 0 writes nothing -- and agreement (within rounding) with
+    the stack's proposal_delta given the same prediction."""
+    values, requests, idx, w, tgt, beta, ld, mass = _token_operands(34, K=1)
+    one_w = torch.ones_like(w)
+    rows = values[requests[:, None, None], torch.arange(values.shape[1])[None, :, None], idx]
+    _, d = torch_oracle.token_propose(values, requests, idx, one_w, tgt, torch.ones_like(beta), ld,
+                                      torch.ones_like(mass))
+    torch.testing.assert_close(rows[..., 0, :] + d.view_as(rows)[..., 0, :], tgt, atol=1e-6, rtol=1e-5)
+    _, d = torch_oracle.token_propose(values, requests, idx, w, tgt, torch.zeros_like(beta), ld,
+                                      torch.ones_like(mass))
+    torch.testing.assert_close(rows + d.view_as(rows), ld.exp()[..., None] * rows, atol=1e-6, rtol=1e-5)
+    _, d = torch_oracle.token_propose(values, requests, idx, w, tgt, beta, ld, torch.zeros_like(mass))
+    assert d.abs().max().item() == 0.0
+    values, requests, idx, w, tgt, beta, ld, mass = _token_operands(35, K=4)
+    rows = values[requests[:, None, None], torch.arange(values.shape[1])[None, :, None], idx]
+    _, d = torch_oracle.token_propose(values, requests, idx, w, tgt, beta, ld, mass)
+    pred = torch_oracle.token_read(values, requests, idx, w)
+    stack = torch_oracle.proposal_delta(rows, w, pred, tgt, beta, ld, mass)
+    torch.testing.assert_close(d.view_as(stack), stack, atol=1e-6, rtol=1e-5)

@@ -153,3 +153,27 @@ def test_window_mask_cache():
     allowed = (kpos <= qpos) & (kpos > qpos - 4)
     assert torch.equal(m == 0, allowed) and torch.isinf(m[~allowed]).all()
     assert _window_mask(3, 5, 4, torch.device("cpu"), torch.float32) is m
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+def test_copied_kv_cache_continues_independently_when_functional(in_place):
+    """With gl_commit_in_place = False the KV cache is functional, as the
+    reference's (S/layers/attention.py:53-58 builds new tensors with torch.cat):
+    two continuations of one cache, stepped alternately, each equal a full pass
+    over their own tokens.  With the in-place decode append (the default) the
+    cache has one owner, so only one continuation is checked."""
+    torch.manual_seed(8)
+    layer = Transformer({**config(), "attention_window": 5, "gl_commit_in_place": in_place}, 0).eval()
+    prompt = torch.randn(1, 6, 32)
+    branch = [torch.randn(1, 5, 32), torch.randn(1, 5, 32)]
+    with torch.no_grad():
+        full = [layer(torch.cat((prompt, b), 1))[:, 6:] for b in branch]
+        cache = {}
+        layer(prompt, cache)
+        caches = [dict(cache), dict(cache)] if not in_place else [cache]
+        outs = [[] for _ in caches]
+        for t in range(5):
+            for c, (cc, out) in enumerate(zip(caches, outs)):
+                out.append(layer(branch[c][:, t:t + 1], cc))
+        for c, out in enumerate(outs):
+            torch.testing.assert_close(torch.cat(out, 1), full[c], atol=1e-6, rtol=1e-5)
