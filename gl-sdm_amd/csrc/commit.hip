@@ -40,6 +40,7 @@
 // addresses whenever its keys keep equal addresses together (keys = addresses,
 // and the stack's addr*(C*L) + pos*L + layer).
 #include <atomic>
+#include <mutex>
 
 #include "glsdm_internal.h"
 
@@ -1409,6 +1410,65 @@ extern "C" int glsdm_overlay_commit(const void *base, int32_t dtype, int64_t B, 
 #undef GLSDM_OVERLAY
 }
 
+// ------------------------------------------------------------ allocation-free commit
+//
+// glsdm_commit_noalloc runs glsdm_commit's kernels with their workspace in a
+// file-scope device array instead of a caller buffer, for callers that cannot
+// allocate.  Each GPU holds its own copy of the array from module load until
+// the process ends; host code addresses it only through the per-device pointer
+// that hipGetSymbolAddress returns (the array's name on the host is not a
+// device address).  Calls on one GPU share the array, so calls that overlap
+// on one GPU race; every call clears the words it needs before use.
+constexpr int64_t NOALLOC_MAX_ENTRIES = (int64_t)1 << 19;      // the workspace then fits in 13 MiB, any rows
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+
+__device__ __attribute__((aligned(256))) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mutex;
+static void *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// The current device's copy of the scratch array (looked up once per device).
+static int scratch_address(void **out)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(GLSDM_ERR_HIP, "commit_noalloc: hipGetDevice failed");
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return fail(GLSDM_ERR_UNSUPPORTED, "commit_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(GLSDM_ERR_HIP, "commit_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return GLSDM_OK;
+}
+
+extern "C" int glsdm_commit_noalloc(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                                    const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                                    const int64_t *keys, int64_t entries, int64_t *unique_out, void *stream)
+{
+    if (rows < 1 || D < 1 || entries < 0)
+        return fail(GLSDM_ERR_ARG, "commit_noalloc: bad shape rows=%lld D=%lld entries=%lld", (long long)rows,
+                    (long long)D, (long long)entries);
+    if (entries > NOALLOC_MAX_ENTRIES)
+        return fail(GLSDM_ERR_UNSUPPORTED, "commit_noalloc: %lld entries exceed the static scratch's limit of %lld",
+                    (long long)entries, (long long)NOALLOC_MAX_ENTRIES);
+    if (entries == 0) return GLSDM_OK;
+    int rc = check_commit("commit_noalloc", rows, D, entries);
+    if (rc) return rc;
+    const size_t need = plan_workspace(nullptr, entries, pass_count(address_bits(rows))).bytes;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(GLSDM_ERR_UNSUPPORTED, "commit_noalloc: %zu scratch bytes needed, %zu available", need,
+                    NOALLOC_SCRATCH_BYTES);
+    void *ws = nullptr;
+    if ((rc = scratch_address(&ws))) return rc;
+    return glsdm_commit(bank, bank_dtype, rows, D, addresses, deltas, delta_dtype, keys, entries, ws,
+                        NOALLOC_SCRATCH_BYTES, unique_out, stream);
+}
+
 extern "C" int glsdm_commit_status(const void *workspace, size_t workspace_bytes, int64_t entries, int64_t rows,
                                    int64_t *status, void *stream)
 {
@@ -1418,6 +1478,12 @@ extern "C" int glsdm_commit_status(const void *workspace, size_t workspace_bytes
     if (entries > 0) {
         int rc = check_commit("commit_status", rows, 1, entries);
         if (rc) return rc;
+        if (!workspace) {                    // the status of glsdm_commit_noalloc on this device
+            void *ws = nullptr;
+            if ((rc = scratch_address(&ws))) return rc;
+            workspace = ws;
+            workspace_bytes = NOALLOC_SCRATCH_BYTES;
+        }
         const CommitWorkspace ws = plan_workspace(const_cast<void *>(workspace), entries,
                                                   pass_count(address_bits(rows)));
         if (!workspace || workspace_bytes < ws.bytes)

@@ -38,6 +38,7 @@ SIGNATURES = {
     "glsdm_commit_prepare": ([_I64, _P, _I64, _P, _SZ, _P], _I32),
     "glsdm_commit_apply": ([_P, _I32, _I64, _I64, _P, _I32, _P, _I64, _P, _SZ, _P, _P], _I32),
     "glsdm_commit_status": ([_P, _SZ, _I64, _I64, _P, _P], _I32),
+    "glsdm_commit_noalloc": ([_P, _I32, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _P], _I32),
     "glsdm_debug_force_lookback_timeout": ([_I32], _I32),
     "glsdm_absolute_addresses": ([_P, _I64, _I64, _I64, _I32, _I64, _P, _P], _I32),
     "glsdm_proposal_keys": ([_P, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),

@@ -195,6 +195,24 @@ int glsdm_commit(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
                  int64_t *unique_out, void *stream);
 
 /*
+ * glsdm_commit without a workspace argument, allocating nothing: its workspace
+ * is a static device array of the library (16 MiB, held on every GPU the
+ * library runs on until the process ends), addressed through the pointer
+ * hipGetSymbolAddress returns for the calling thread's current device, which
+ * must be the stream's device.  Same arguments and results as glsdm_commit,
+ * bit for bit, for entries <= 2^19 (524,288, one config-2 epoch); larger
+ * commits return GLSDM_ERR_UNSUPPORTED before any launch.  It calls no
+ * hipMalloc or hipFree.  Calls on one GPU share the array: calls that overlap
+ * on one GPU (several streams or threads) race and must be serialised by the
+ * caller.  Status: glsdm_commit_status with a NULL workspace.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ */
+int glsdm_commit_noalloc(void *bank, int32_t bank_dtype, int64_t rows, int64_t D,
+                         const int64_t *addresses, const void *deltas, int32_t delta_dtype,
+                         const int64_t *keys, int64_t entries, int64_t *unique_out, void *stream);
+
+/*
  * glsdm_commit in two steps: glsdm_commit_prepare groups the entries by address
  * (the sort; it reads only the addresses, never the bank) into the workspace,
  * and glsdm_commit_apply, later on any stream ordered after it, runs the
@@ -222,7 +240,8 @@ int glsdm_commit_apply(void *bank, int32_t bank_dtype, int64_t rows, int64_t D, 
  *              gave up) / bit 1 (inconsistent bucket pieces); when non-zero the
  *              call wrote no bank row;
  *   status[1]: the number of entries dropped for an address outside [0, rows).
- * entries == 0 reports zeros (no workspace needed).
+ * entries == 0 reports zeros (no workspace needed).  workspace NULL: the status
+ * of the last glsdm_commit_noalloc on the calling thread's current device.
  * No counterpart in the reference: its sort cannot fail and its torch indexing
  * raises on an out-of-range address (flat[unique] and index_copy of
  * S/memory/transactions.py:96); a caller that wants that behaviour raises on
