@@ -114,16 +114,17 @@ def make_write_operands(cfg, seed=1):
 class Pipeline:
     """Preallocated buffers and direct C-ABI calls for the 4-epoch workload.
 
-    Two schedules of the same work:
-    * serial (the timed default): every call on one stream, epoch after epoch;
-    * overlapped (--schedule overlap): scoring+routing never reads the bank, so
-      the route stream computes epoch e+1's read and write routes and proposal
-      keys while the memory stream runs epoch e's read and commit.  The memory
-      stream waits for an epoch's routes with an event; read(e+1) follows
-      commit(e) in stream order, so every read still sees the bank version of
-      its epoch.  Measured on MI355X it gains ~2%: the concurrent kernels slow
-      each other down by almost as much as they overlap (and their individual
-      durations stop being a clean roofline measurement), so it is not the default.
+    Two schedules of the same work (``--schedule``; ``auto`` picks overlap when a
+    step has more than one epoch, serial otherwise):
+    * overlap: scoring+routing never reads the bank, so the route stream
+      computes epoch e+1's read and write routes and proposal keys while the
+      memory stream runs epoch e's read and commit.  The memory stream waits for
+      an epoch's routes with an event; read(e+1) follows commit(e) in stream
+      order, so every read still sees the bank version of its epoch.  Routing is
+      VALU-bound and read/commit HBM-bound, so the two streams share the CUs;
+    * serial: every call on one stream, epoch after epoch (one-epoch steps gain
+      nothing from the cross-stream waits).  The per-call durations reported
+      next to the step time come from a separate serial pass.
     """
 
     def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False):
