@@ -389,37 +389,56 @@ def literal_scoring(cfg, dev, reps=20):
             "note": "the reference's router.q Linear (hipBLASLt) and the route of its bf16 output, per epoch"}
 
 
-def cpu_baseline(cfg, budget_s=12.0):
-    """Scalar C oracle (oracle/glsdm_oracle.c, 1 thread) on a bounded sample of the
-    same workload: whole epochs for request 0, repeated until ~budget_s."""
-    from oracle import c_oracle
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """The reference's CPU path, timed on the host cores: ``oracle/torch_oracle``,
+    the reference's own torch op sequence (factor scores q @ K^T per head; route
+    and read of S/memory/routing.py:10-28; the keyed stable sort, segment_reduce
+    and index_copy of S/memory/transactions.py:89-96, a new bank per commit),
+    fp32 (the reference's only state dtype) on the workload's bf16-rounded
+    inputs, all B requests, torch's intra-op threads.  One warmup epoch, then
+    whole epochs until ``budget_s``; tokens/s = B*C / median epoch time
+    (P/scripts/benchmark_memory.py:82-97 takes the median too)."""
+    from oracle import torch_oracle
     keys, bank, qr, qw, delta = make_inputs(cfg)
-    C, H, half, D, k = (cfg[x] for x in ("C", "H", "half", "D", "k"))
-    S = half * half
-    bank0 = bank.float().reshape(1, H, S, D)   # request 0's replica
-    flat = bank0.reshape(-1, D).clone()
-    tokens, t0, e = 0, time.perf_counter(), 0
-    while True:
+    B, C, H, half, D, k = (cfg[x] for x in ("B", "C", "H", "half", "D", "k"))
+    epochs = cfg["T"] // C
+    values = bank.float().unsqueeze(0).expand(B, -1, -1, -1).contiguous()     # per-request replicas
+    kf = keys.float()
+    pos = torch.arange(C).view(1, C, 1, 1).expand(B, C, H, k).reshape(-1)
+
+    def epoch(e, values):
         sl = slice(e * C, (e + 1) * C)
-        sr = c_oracle.score(qr[:1, sl], keys)
-        idx, w = c_oracle.route(sr, k)
-        c_oracle.read(flat.view(1, H, S, D), idx, w)
-        sw = c_oracle.score(qw[:1, sl], keys)
-        widx, _ = c_oracle.route(sw, k)
-        addr = (torch.arange(H).view(1, 1, H, 1) * S + widx).reshape(-1)
-        ck = addr * C + torch.arange(C).view(1, C, 1, 1).expand(1, C, H, k).reshape(-1)
-        lib = c_oracle.lib()
-        d = delta[:1, sl].float().reshape(-1, D).contiguous()
-        lib.oracle_commit(flat.data_ptr(), flat.shape[0], D, addr.data_ptr(), d.data_ptr(), ck.data_ptr(),
-                          addr.numel())
-        tokens += C
-        e = (e + 1) % (cfg["T"] // C)
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": tokens / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"request 0 of the workload, {tokens} tokens ({tokens // C} epochs of 512): "
-                      f"scoring + route + read + route + commit, fp32 scalar C oracle, {dt:.1f} s"}
+        _, idx, w = torch_oracle.routed_read(values, torch.einsum("bthe,hle->bthl", qr[:, sl].float(), kf), k)
+        widx, _ = torch_oracle.route(torch.einsum("bthe,hle->bthl", qw[:, sl].float(), kf), k)
+        addr = torch_oracle.absolute_addresses(values, widx).reshape(-1)
+        new = torch_oracle.commit(values.reshape(-1, D), addr, delta[:, sl].float().reshape(-1, D), addr * C + pos)
+        return new.view_as(values)
+
+    values = epoch(0, values)                                                   # warmup
+    times, e, t0 = [], 1, time.perf_counter()
+    while len(times) < 2 or time.perf_counter() - t0 < budget_s:
+        t = time.perf_counter()
+        values = epoch(e % epochs, values)
+        times.append(time.perf_counter() - t)
+        e += 1
+    med = statistics.median(times)
+    return {"value": B * C / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": f"{len(times)} whole epochs of the workload after 1 warmup (B={B} requests x {C} tokens "
+                      f"each; score + route + read + write route + commit with a new bank per commit), "
+                      f"median {med:.3f} s per epoch; oracle/torch_oracle: the reference's torch op sequence, "
+                      f"fp32, {torch.get_num_threads()} threads"}
 
 
 # BASELINE.json configs[3] and configs[4]: the physical stack (S/layers/stack.py) with
@@ -636,7 +655,7 @@ def main():
                          "anyway, and the cross-stream waits only add latency)")
     ap.add_argument("--compare-schedules", action="store_true",
                     help="also time the other schedule (reported as ms_per_step_other_schedule)")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-full-stack", action="store_true",
                     help="skip the config-4 full-stack forward reported beside the headline line")
     ap.add_argument("--backward", action="store_true",

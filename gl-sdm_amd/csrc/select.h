@@ -224,21 +224,23 @@ __device__ __forceinline__ void group_top(int n, int g, KeyOf key_of, KT (&t)[K]
 
 constexpr int STAIR_MAX = 280;   // |P| for width 64 (sum over n <= 64 of floor(64 / n))
 
-// Builds the staircase cells (i << 8 | j) of P for (kk, width) in LDS; every
-// thread of the block calls it, the caller synchronises before use.
+// Builds the staircase cells (i << 8 | j) of P for (kk, width) in LDS;
+// every thread of the block calls it, the caller synchronises before use.
+// Lane i of each wavefront takes row i's length (kk <= 64); a shuffle scan
+// gives the row offsets, and the first wavefront writes the cells.
 __device__ __forceinline__ int staircase_build(uint16_t *pairs, int kk, int width)
 {
-    const int i = threadIdx.x;
-    int total = 0, offset = 0;
-    for (int r = 0; r < kk; ++r) {
-        const int len = min(kk, width / (r + 1));
-        if (r < i) offset += len;
-        total += len;
+    const int i = threadIdx.x & 63;
+    const int len = i < kk ? min(kk, width / (i + 1)) : 0;
+    int incl = len;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off);
+        if (i >= off) incl += y;
     }
-    if (i < kk) {
-        const int len = min(kk, width / (i + 1));
-        for (int j = 0; j < len; ++j) pairs[offset + j] = (uint16_t)((i << 8) | j);
-    }
+    const int total = __shfl(incl, 63);
+    if (threadIdx.x < 64)
+        for (int j = 0; j < len; ++j) pairs[incl - len + j] = (uint16_t)((i << 8) | j);
     return total;
 }
 

@@ -98,3 +98,54 @@ def test_score_route_keys_equals_route_then_keys(device, split, B, T, H, half, w
     assert torch.equal(addr, raddr) and torch.equal(keys, rkeys)
     pos = torch.arange(offset, offset + T, device=device).view(1, T, 1, 1)
     assert torch.equal(keys, addr * (chunk * layers) + pos * layers + layer)
+
+
+def _check_filtered(device, q, k, width, tie):
+    """The filtered K = 16 kernel (taken without score export) against the
+    unfiltered kernel's exported scores and the oracle routing them."""
+    qd, kd = q.to(device), k.to(device)
+    idx, w, none = hip.score_route(qd, kd, width, tie, split=False)
+    assert none is None
+    ridx, rw, scores = hip.score_route(qd, kd, width, tie, export_scores=True, split=False)
+    assert torch.equal(idx, ridx)
+    torch.testing.assert_close(w, rw, atol=0, rtol=0, equal_nan=True)     # bitwise; NaN rows stay NaN
+    oidx, ow = c_oracle.route(scores.cpu(), width, tie)
+    assert torch.equal(idx.cpu(), oidx)
+    torch.testing.assert_close(w.cpu(), ow, atol=2e-7, rtol=2e-6, equal_nan=True)
+
+
+@pytest.mark.parametrize("tie", ["highest", "lowest"])
+@pytest.mark.parametrize("B,T,H,dk,half,width", [
+    (8, 512, 8, 128, 256, 16),     # config 2's epoch
+    (1, 77, 3, 64, 64, 9),         # one chunk per factor, ragged tokens
+    (2, 45, 2, 256, 128, 12),
+    (1, 130, 1, 128, 320, 16),     # five chunks: a partial group of maxima
+    (1, 64, 2, 64, 512, 15),
+])
+def test_filtered_route_matches_unfiltered_and_oracle(device, tie, B, T, H, dk, half, width):
+    q, k = _inputs(B, T, H, dk, half, seed=3 * T + half + width + dk)
+    _check_filtered(device, q, k, width, tie)
+
+
+@pytest.mark.parametrize("tie", ["highest", "lowest"])
+def test_filtered_route_overflow_falls_back_exactly(device, tie):
+    """Near-duplicate sub-keys (many equal and close scores), zero queries (every
+    score ties) and a block mixing both with ordinary tokens: tokens whose
+    survivors overflow the buffer make the block select unfiltered."""
+    q, k = _inputs(2, 96, 2, 128, 256, seed=41, clusters=True)
+    _check_filtered(device, q, k, 16, tie)
+    q, k = _inputs(1, 64, 1, 128, 256, seed=42)
+    _check_filtered(device, torch.zeros_like(q), k, 16, tie)
+    q[0, 10:20] = 0
+    _check_filtered(device, q, k, 16, tie)
+
+
+def test_filtered_route_non_finite_rows(device):
+    """Rows whose queries hold NaN (every score NaN) or huge values (infinite
+    scores) route as the unfiltered kernel and the oracle do (NaN ranks highest)."""
+    q, k = _inputs(1, 70, 2, 128, 256, seed=43)
+    q = q.float()
+    q[0, 3, 0, 5] = float("nan")
+    q[0, 7, 1] *= 1e38
+    q[0, 9, 0, :4] = float("inf")
+    _check_filtered(device, q.bfloat16(), k, 16, "highest")
