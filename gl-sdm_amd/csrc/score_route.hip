@@ -703,8 +703,13 @@ __global__ __launch_bounds__(256) void score_route16_kernel(const bf16_t *__rest
     }
     const int64_t out_row = (live ? row_n : 0) * H + h;
     const KeyRow kr = ka.addr ? key_row(ka, out_row, H, width) : KeyRow{nullptr, nullptr, 0, 0, 0};
-    route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, TIE, g, s_pairs, npairs,
-                     finite, live, index + out_row * width, weights + out_row * width, kr);
+    __syncthreads();                          // the stashed lists are read across lanes of the token
+    if (width == K && half <= 32768)
+        route_tail16(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, TIE, g, s_pairs, finite, live,
+                     index + out_row * width, weights + out_row * width, kr);
+    else
+        route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, TIE, g, s_pairs,
+                         npairs, finite, live, index + out_row * width, weights + out_row * width, kr);
 }
 
 template <int DK>

@@ -425,6 +425,74 @@ __device__ __forceinline__ void route_tail(const uint32_t *i0, const float *v0, 
     }
 }
 
+// route_tail for width == 16 with factor lists of 16 (kk = 16) and slots in 30
+// bits, G = 4: the staircase of P is fixed (rows of 16, 8, 5, 4, 3, 2, 2, 2
+// and eight of 1 cells, 50 in all), so lane g takes a fixed set of at most 15
+// cells -- columns j = g (mod 4) of rows 0-7 and column 0 of rows 8+g and 12+g
+// -- read from the stashed lists without a pairs table, keyed exactly as
+// CellKeyD does (finite factor scores: their sums are never NaN).  The
+// verification and the full-grid fallback are candidate_top's.
+__device__ __forceinline__ void route_tail16(const uint32_t *i0, const float *v0, const uint32_t *i1, const float *v1,
+                                             int half, int tie, int g, const uint16_t *pairs, bool finite, bool live,
+                                             int64_t *index_row, float *weight_row, const KeyRow &kr)
+{
+    constexpr int K = 16, G = 4, W = 16;
+    int ib = 1;
+    while ((1ll << ib) < (int64_t)half * half) ++ib;
+    const CellKeyD ck{tie, ib, 30 - ib, (uint32_t)((1ull << ib) - 1ull)};
+    double t[K];
+    bool exact = false;
+    if (finite) {
+        auto cell = [&](float a, uint32_t ia, float b, uint32_t jb) -> double {
+            const uint32_t x = __float_as_uint((a + b) + 0.0f);              // -0 folded onto +0
+            const uint32_t ob = x ^ (uint32_t)(((int32_t)x >> 31) | (int32_t)0x80000000);
+            const uint32_t slot = ia * (uint32_t)half + jb;
+            const uint32_t tb = tie == GLSDM_TIE_HIGHEST ? slot : ck.imask - slot;
+            return __hiloint2double((int)((ob >> 2) + 0x00100000u), (int)((ob << 30) | (tb << ck.shift)));
+        };
+        float w1[4];
+        uint32_t x1[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            w1[q] = v1[g + 4 * q];
+            x1[q] = i1[g + 4 * q];
+        }
+        const float b0 = v1[0];
+        const uint32_t jb0 = i1[0];
+        double c[K];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = cell(v0[0], i0[0], w1[q], x1[q]);        // row 0
+        c[4] = cell(v0[1], i0[1], w1[0], x1[0]);                                      // row 1: j = g, g + 4
+        c[5] = cell(v0[1], i0[1], w1[1], x1[1]);
+        c[6] = cell(v0[2], i0[2], w1[0], x1[0]);                                      // row 2: j = g, and 4
+        c[7] = g == 0 ? cell(v0[2], i0[2], w1[1], x1[1]) : 0.0;
+        c[8] = cell(v0[3], i0[3], w1[0], x1[0]);                                      // row 3
+        c[9] = g < 3 ? cell(v0[4], i0[4], w1[0], x1[0]) : 0.0;                        // row 4
+        c[10] = g < 2 ? cell(v0[5], i0[5], w1[0], x1[0]) : 0.0;                       // rows 5-7
+        c[11] = g < 2 ? cell(v0[6], i0[6], w1[0], x1[0]) : 0.0;
+        c[12] = g < 2 ? cell(v0[7], i0[7], w1[0], x1[0]) : 0.0;
+        c[13] = cell(v0[8 + g], i0[8 + g], b0, jb0);                                  // rows 8-15: j = 0
+        c[14] = cell(v0[12 + g], i0[12 + g], b0, jb0);
+        c[15] = 0.0;
+        list_first<K>(t, c);
+        group_merge<K, G>(t);
+        // verify: the first excluded cell of each row (column len_i) scores below the 16th pick
+        const uint32_t tau = ck.order(t[W - 1]);
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = g + 4 * q;
+            const int j = i == 0 ? W : i == 1 ? 8 : i == 2 ? 5 : i == 3 ? 4 : i == 4 ? 3 : i < 8 ? 2 : 1;
+            if (j < W) ok = ok && order_bits(v0[i] + v1[j]) < tau;
+        }
+        const uint64_t bad = __ballot(!ok);
+        const int lane = threadIdx.x & 63;
+        exact = ((bad >> (lane & ~(G - 1))) & 0xFull) == 0;
+    }
+    if (!exact) candidate_top<K, G>(i0, v0, i1, v1, half, W, ck, g, pairs, 0, false, t);
+    finish_route<K, G>(t, ck, W, g, live, index_row, weight_row, kr);
+}
+
 // Stashes the top-kk of a factor list (indices and scores) for the candidate
 // stage; returns whether all kk scores are finite.
 template <int K, int G, typename KT>
