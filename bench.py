@@ -127,10 +127,13 @@ class Pipeline:
       next to the step time come from a separate serial pass.
     """
 
-    def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False):
+    def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False, split_commit=False):
         from glsdm import _native as N
         self.N, self.cfg, self.dev, self.write_path, self.backward = N, cfg, device, write_path, backward
         self.overlay = overlay
+        if split_commit and (overlay or write_path != "deltas"):
+            raise SystemExit("--split-commit runs the dense bank with synthetic deltas only")
+        self.split_commit = split_commit
         keys, bank, qr, qw, delta = make_inputs(cfg)
         B, T, C, H, half, dk, D, k = (cfg[x] for x in ("B", "T", "C", "H", "half", "dk", "D", "k"))
         self.epochs = T // C
@@ -148,6 +151,10 @@ class Pipeline:
         size = ctypes.c_size_t(0)
         N.call("glsdm_commit_workspace_bytes", self.E, self.rows, ctypes.byref(size))
         self.ws = torch.empty(size.value, dtype=torch.uint8, device=device)
+        # split commit: one workspace per epoch, since the route stream sorts epoch e+1's
+        # entries while the memory stream still applies epoch e's from its workspace
+        self.cws = [torch.empty(size.value, dtype=torch.uint8, device=device)
+                    for _ in range(self.epochs if split_commit else 0)]
         N.call("glsdm_score_route_workspace_bytes", B, C, H, half, k, ctypes.byref(size))
         # one route workspace: both routing calls of an epoch run on the same stream, one after the other
         self.route_ws = torch.empty(max(size.value, 8), dtype=torch.uint8, device=device)
@@ -212,7 +219,14 @@ class Pipeline:
             p(self.widx[e]), p(self.ww[e]), p(self.addr[e]), p(self.ckeys[e]), p(self.route_ws),
             self.route_ws.numel(), st))
 
-    def memory(self, e, stream, count_unique=False):
+    def prepare(self, e, stream):
+        """Split commit, first half: group epoch e's entries by address (reads only
+        the write route's addresses, never the bank) into the epoch's workspace."""
+        N, p, st = self.N, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
+        self._timed("commit_prepare", stream, lambda: N.call(
+            "glsdm_commit_prepare", self.rows, p(self.addr[e]), self.E, p(self.cws[e]), self.cws[e].numel(), st))
+
+    def memory(self, e, stream, count_unique=False, split=False):
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, D, k = (c[x] for x in ("B", "C", "H", "half", "D", "k"))
         dt = N.dtype_code(self.base if self.overlay else self.bank)
@@ -245,6 +259,11 @@ class Pipeline:
             self._timed("read_bw_rows", stream, lambda: N.call(
                 "glsdm_read_backward_rows", p(self.grad_bank), H * S, D, p(self.fold[e]), self.E, k,
                 p(self.w[e]), p(self.grad_out), p(self.bw_ws), self.bw_ws.numel(), st))
+        if self.write_path == "deltas" and split:
+            self._timed("commit", stream, lambda: N.call(
+                "glsdm_commit_apply", p(self.bank), dt, self.rows, D, p(self.delta[e]), dt, p(self.ckeys[e]),
+                self.E, p(self.cws[e]), self.cws[e].numel(), uq, st))
+            return
         if self.write_path == "deltas":
             self._timed("commit", stream, lambda: N.call(
                 "glsdm_commit", p(self.bank), dt, self.rows, D, p(self.addr[e]), p(self.delta[e]), dt,
@@ -291,10 +310,12 @@ class Pipeline:
         for e in range(self.epochs):
             rs.wait_event(self.consumed[e])   # the previous step's read/commit of epoch e is done with its routes
             self.routes(e, rs)
+            if self.split_commit:
+                self.prepare(e, rs)
             self.routed[e].record(rs)
         for e in range(self.epochs):
             ms.wait_event(self.routed[e])
-            self.memory(e, ms)
+            self.memory(e, ms, split=self.split_commit)
             self.consumed[e].record(ms)
 
     def unique_rows(self):
@@ -452,7 +473,7 @@ STACK_CONFIGS = {
     # 64 streams of a 2^20-slot bank: bf16 request snapshots (64 x 2 GiB)
     5: dict(STACK, gl_slots=1048576, gl_state_dtype="bfloat16", B=64, prompt=512, decode_steps=4096),
 }
-MEMORY_CALLS = ("routed_snapshot_read", "proposal_keys", "proposal_error", "commit_proposals")
+MEMORY_CALLS = ("routed_snapshot_read", "commit_proposals")     # + ProposalLog.append (the proposals)
 
 
 def stack_flops_per_token(cfg):
@@ -584,9 +605,10 @@ def stack_main(args, dev):
         end.record()
         torch.cuda.synchronize()
         ms = start.elapsed_time(end) / args.steps
-        with CallTimer(hip, MEMORY_CALLS) as timer:
+        from glsdm.memory import ProposalLog
+        with CallTimer(hip, MEMORY_CALLS) as timer, CallTimer(ProposalLog, ("append",)) as appends:
             model.prefill(inputs)
-        mem = timer.totals(1)
+        mem = {**timer.totals(1), **{"proposal_append": v for v in appends.totals(1).values()}}
         flops = per_token * B * T
         result = dict(base, value=round(B * T / (ms * 1e-3), 1), steps=args.steps, warmup=args.warmup,
                       ms_per_step=round(ms, 3),
@@ -601,7 +623,38 @@ def stack_main(args, dev):
         print(json.dumps(result))
         return
     # config 5: prompt prefill, then one-token decode steps with a commit every 512 tokens
-    P, steps = cfg["prompt"], args.decode_steps or cfg["decode_steps"]
+    steps = args.decode_steps or cfg["decode_steps"]
+    decode = decode_run(model, cfg, dev, steps)
+    p50 = decode["p50_ms"]
+    result = dict(base, value=round(B / (p50 * 1e-3), 1), steps=steps, warmup=0, ms_per_step=p50,
+                  higher_is_better=True,
+                  config={"workload": workload + f"; {B} streams, {cfg['prompt']}-token prompt, {steps} decode "
+                          "steps of one token per stream, commit every 512 steps", "B": B, "prompt": cfg["prompt"],
+                          "decode_steps": steps, "slots": cfg["gl_slots"], "parallelism": "single GPU"},
+                  decode=decode, roofline=None)
+    print(json.dumps(result))
+
+
+def decode_record(dev):
+    """Config 5 decode, reported beside the headline line:
+    all of the config's decode steps (bench.py --config 5 reports it alone)."""
+    cfg = STACK_CONFIGS[5]
+    model = stack_model(cfg, dev)
+    out = decode_run(model, cfg, dev, cfg["decode_steps"])
+    del model
+    torch.cuda.empty_cache()
+    out["workload"] = ("BASELINE configs[4]: 16-layer stack (8 global, M=2^20, k=16, bf16 request snapshots), "
+                       "d_model 1024, 64 streams, 512-token prompt then 4096 one-token decode steps, a commit "
+                       "every 512; bf16 random init")
+    return out
+
+
+def decode_run(model, cfg, dev, steps):
+    """Config 5's decode: the prompt's prefill (one commit), then ``steps`` one-token
+    decode steps of every stream (a commit every 512 tokens); per-step times from
+    HIP events on the current stream, so each step's host work and launches are in it."""
+    B, P = cfg["B"], cfg["prompt"]
+    g = torch.Generator("cpu").manual_seed(0)
     prompt = torch.randint(cfg["vocab_size"], (B, P), generator=g).to(dev)
     tokens = torch.randint(cfg["vocab_size"], (B, steps), generator=g).to(dev)
     torch.cuda.synchronize()
@@ -619,22 +672,21 @@ def stack_main(args, dev):
     marks[steps].record()
     torch.cuda.synchronize()
     dur = [marks[s].elapsed_time(marks[s + 1]) for s in range(steps)]
-    plain = sorted(d for s, d in enumerate(dur) if s not in set(commit_steps))
+    in_commit = set(commit_steps)
+    plain = sorted(d for s, d in enumerate(dur) if s not in in_commit)
     commits = [dur[s] for s in commit_steps]
-    p50 = statistics.median(dur)
-    result = dict(base, value=round(B / (p50 * 1e-3), 1), steps=steps, warmup=0, ms_per_step=round(p50, 4),
-                  higher_is_better=True,
-                  config={"workload": workload + f"; {B} streams, {P}-token prompt, {steps} decode steps of one "
-                          "token per stream, commit every 512 steps", "B": B, "prompt": P, "decode_steps": steps,
-                          "slots": cfg["gl_slots"], "parallelism": "single GPU"},
-                  decode={"p50_ms": round(p50, 4), "p50_ms_without_commit": round(statistics.median(plain), 4),
-                          "p90_ms": round(sorted(dur)[int(0.9 * steps)], 4),
-                          "commit_steps": len(commits),
-                          "commit_step_ms_mean": round(statistics.mean(commits), 3) if commits else None,
-                          "commit_step_ms_max": round(max(commits), 3) if commits else None,
-                          "commit_entries": B * 512 * 8 * 16 * 16, "prefill_s": round(prefill_s, 3)},
-                  roofline=None)
-    print(json.dumps(result))
+    n_global = sum(p == "global" for p in cfg["gl_layer_pattern"]) * cfg["num_hidden_layers"] \
+        // len(cfg["gl_layer_pattern"])
+    heads = cfg["hidden_size"] // cfg["head_dim"]
+    return {"streams": B, "prompt": P, "decode_steps": steps,
+            "p50_ms": round(statistics.median(dur), 4), "p50_ms_without_commit": round(statistics.median(plain), 4),
+            "p90_ms": round(sorted(dur)[int(0.9 * steps)], 4),
+            "tokens_per_s_at_p50": round(B / (statistics.median(dur) * 1e-3), 1),
+            "commit_steps": len(commits),
+            "commit_step_ms_mean": round(statistics.mean(commits), 3) if commits else None,
+            "commit_step_ms_max": round(max(commits), 3) if commits else None,
+            "commit_entries": B * cfg["gl_chunk_size"] * n_global * heads * cfg["gl_writes"],
+            "prefill_s": round(prefill_s, 3)}
 
 
 def main():
@@ -658,6 +710,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-full-stack", action="store_true",
                     help="skip the config-4 full-stack forward reported beside the headline line")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-5 decode record reported beside the headline line")
     ap.add_argument("--backward", action="store_true",
                     help="also run the read's backward every epoch: weights' and factor scores' gradients, and "
                          "the bank rows' gradient folded into the learned [H, S, D] bank (reported alongside; "
@@ -669,6 +723,10 @@ def main():
                     help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
                          "path with the fused proposal commit; proposals-materialised: the same work with "
                          "gathered rows and stored fp32 deltas")
+    ap.add_argument("--split-commit", action="store_true",
+                    help="overlap schedule: sort each epoch's write entries on the route stream "
+                         "(glsdm_commit_prepare) and apply them on the memory stream (glsdm_commit_apply); "
+                         "the serial pass keeps the one-call glsdm_commit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the timed region, copy 256 MiB device-to-device 3 times (a kernel of known "
                          "traffic for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -685,7 +743,7 @@ def main():
         stack_main(args, dev)
         return
     cfg = CONFIGS[args.config]
-    pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay")
+    pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay", args.split_commit)
     if args.schedule == "auto":
         args.schedule = "overlap" if pipe.epochs > 1 else "serial"
     unique = pipe.unique_rows()
@@ -763,6 +821,11 @@ def main():
         entry = "glsdm_commit_proposals" if args.write_path == "proposals" else "glsdm_commit"
         steps = ("tile bucketing + bucket sort + segment" if pipe.rows >= 1 << 16
                  else "prep + pack + LSD passes + segment")
+        one_call = f"{entry} ({steps})"
+        if pipe.split_commit and args.schedule == "overlap":
+            # the timed launch is the apply; the sort (which reads the addresses) ran on the route stream
+            bytes_launch -= pipe.E * 8
+            entry, steps = "glsdm_commit_apply", "segment; sort by glsdm_commit_prepare on the route stream"
         roof = {"kernel": f"{entry} ({steps})", "bound": "hbm",
                 "unit": "GB/s",
                 "peak": HBM_PEAK / 1e9}
@@ -781,8 +844,11 @@ def main():
                  "ms_per_launch": round(t_timed, 5)})
     roof_iso = None
     if bytes_launch is not None:
-        a_iso = bytes_launch / (isolated_ms * 1e-3) / 1e9
-        roof_iso = {"kernel": roof["kernel"], "achieved": round(a_iso, 1), "frac": round(a_iso / roof["peak"], 4),
+        # the serial pass runs the one-call commit: all of its bytes
+        b_iso = statistics.mean(commit_b) if dominant == "commit" else bytes_launch
+        a_iso = b_iso / (isolated_ms * 1e-3) / 1e9
+        roof_iso = {"kernel": one_call if dominant == "commit" else roof["kernel"],
+                    "achieved": round(a_iso, 1), "frac": round(a_iso / roof["peak"], 4),
                     "ms_per_launch": round(isolated_ms, 5),
                     "note": "the same call alone on one stream (serial pass); `roofline` is measured in the "
                             "timed region, where the route stream's kernels run beside it"}
@@ -799,6 +865,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "schedule": args.schedule,
+        "split_commit": pipe.split_commit and args.schedule == "overlap",
         "ms_per_step_other_schedule": None if ms_other is None else round(ms_other, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -840,9 +907,13 @@ def main():
         "read_commit_frac_of_copy": round(alg_total / rc_time / copy, 4),
         "note": "1 GiB device-to-device copy (read + write bytes / time): the streaming rate this MI355X "
                 "sustains; the fractions above are of the 8 TB/s nominal peak"}
-    if args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense" \
-            and not args.no_full_stack:
+    headline = args.config == 2 and args.write_path == "deltas" and not args.backward and args.bank == "dense"
+    if headline and not args.no_full_stack:
         result["full_stack"] = full_stack_rate(dev)
+    if headline and not args.no_decode:
+        del pipe
+        torch.cuda.empty_cache()
+        result["decode"] = decode_record(dev)
     if args.copy_calibration:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)

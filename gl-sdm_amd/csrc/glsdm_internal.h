@@ -166,6 +166,19 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask)
     return ((uint64_t)hi << 32) | lo;
 }
 
+// The write gates of a global layer's proposal (S/layers/global_layer.py:48-49)
+// from the beta and decay projections' outputs b and d, in fp32:
+// beta = sigmoid(b) = 1 / (1 + exp(-b)) and log_decay = -softplus(d - 4) with
+// softplus(v) = v above 20, else log1p(exp(v)).
+__device__ __forceinline__ void write_gate_values(float b, float d, float &beta, float &log_decay)
+{
+#pragma clang fp contract(off)
+    beta = 1.0f / (1.0f + expf(-b));
+    const float v = d - 4.0f;
+    const float sp = v > 20.0f ? v : log1pf(expf(v));
+    log_decay = -sp;
+}
+
 // Load `VEC` consecutive elements of type T starting at p (16-byte aligned when
 // VEC*sizeof(T) == 16) and widen them to fp32.
 template <typename T, int VEC> struct VecLoad;

@@ -54,6 +54,61 @@ __global__ __launch_bounds__(256) void proposal_error_kernel(int64_t R, int64_t 
     }
 }
 
+// The proposal log's append step, the inference path of a global layer's write
+// proposal (S/layers/global_layer.py:33-54 after its write route): one
+// wavefront per proposal row r = (b*T + t)*H + h writes, at the log's fill,
+//   decay[r] = exp(log_decay), the error row beta * (target - decay * prediction)
+// with beta and log_decay the write gates of the beta/decay projections'
+// outputs (write_gate_values), and for each of its `width` picks the absolute
+// address (b*H + h)*S + slot, the collision key addr*(C*L) + (offset + t)*L +
+// layer and the route weight.  Bit for bit what write_gates, proposal_keys and
+// proposal_error produce one after another.
+template <typename TT, typename TG, int VEC, int CH>
+__global__ __launch_bounds__(256) void proposal_append_kernel(
+    int64_t R, int64_t T, int64_t H, int width, int64_t S, int64_t D, int nv, int64_t offset, int64_t scale,
+    int64_t layers, int64_t layer, const int64_t *__restrict__ index, const float *__restrict__ weights,
+    const float *__restrict__ prediction, const TT *__restrict__ target, const TG *__restrict__ b_in,
+    const TG *__restrict__ d_in, int64_t *__restrict__ addresses, int64_t *__restrict__ keys,
+    float *__restrict__ weights_out, float *__restrict__ error, float *__restrict__ decay)
+{
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= R) return;   // wave-uniform
+    float bv[1], dv[1], bet, ld;
+    VecLoad<TG, 1>::load(b_in + r, bv);
+    VecLoad<TG, 1>::load(d_in + r, dv);
+    write_gate_values(bv[0], dv[0], bet, ld);
+    const float g = expf(ld);
+    if (lane == 0) decay[r] = g;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int v = lane + c * 64;
+        if (v < nv) {
+            float tg[VEC], pr[VEC], er[VEC];
+            VecLoad<TT, VEC>::load(target + r * D + (int64_t)v * VEC, tg);
+            VecLoad<float, VEC>::load(prediction + r * D + (int64_t)v * VEC, pr);
+#pragma unroll
+            for (int x = 0; x < VEC; ++x) {
+                const float gp = g * pr[x];
+                const float diff = tg[x] - gp;
+                er[x] = bet * diff;
+            }
+            VecStore<float, VEC>::store(error + r * D + (int64_t)v * VEC, er);
+        }
+    }
+    const int64_t h = r % H, bt = r / H;
+    const int64_t t = bt % T, b = bt / T;
+    const int64_t row0 = (b * H + h) * S;
+    for (int j = lane; j < width; j += 64) {
+        const int64_t i = r * width + j;
+        const int64_t a = row0 + index[i];
+        addresses[i] = a;
+        keys[i] = a * scale + (offset + t) * layers + layer;
+        weights_out[i] = weights[i];
+    }
+}
+
 template <typename TR, typename TT, int VEC, int CH>
 __global__ __launch_bounds__(256) void proposal_delta_kernel(
     int64_t R, int width, int64_t D, int nv, const TR *__restrict__ rows, const float *__restrict__ weights,
@@ -152,6 +207,38 @@ static void launch_error(int64_t R, int64_t D, int nv, int ch, const float *pred
 #undef GLSDM_ERR_LAUNCH
 }
 
+struct AppendArgs {
+    int64_t R, T, H;
+    int width;
+    int64_t S, D, offset, scale, layers, layer;
+    const int64_t *index;
+    const float *weights, *prediction;
+    const void *target, *b_in, *d_in;
+    int64_t *addresses, *keys;
+    float *weights_out, *error, *decay;
+};
+
+template <typename TT, typename TG, int VEC>
+static void launch_append(const AppendArgs &a, int nv, int ch, hipStream_t st)
+{
+    const dim3 grid((unsigned)ceil_div(a.R, 4)), block(256);
+    const TT *tg = static_cast<const TT *>(a.target);
+    const TG *bi = static_cast<const TG *>(a.b_in), *di = static_cast<const TG *>(a.d_in);
+#define GLSDM_APPEND_LAUNCH(C)                                                                                 \
+    hipLaunchKernelGGL((proposal_append_kernel<TT, TG, VEC, C>), grid, block, 0, st, a.R, a.T, a.H, a.width, a.S, \
+                       a.D, nv, a.offset, a.scale, a.layers, a.layer, a.index, a.weights, a.prediction, tg, bi, di,  \
+                       a.addresses, a.keys, a.weights_out, a.error, a.decay)
+    GLSDM_CH_SWITCH(ch, GLSDM_APPEND_LAUNCH)
+#undef GLSDM_APPEND_LAUNCH
+}
+
+template <typename TT, typename TG>
+static void launch_append_t(const AppendArgs &a, const ProposalPlan &p, hipStream_t st)
+{
+    if (p.vec == 4) launch_append<TT, TG, 4>(a, p.nv, p.ch, st);
+    else launch_append<TT, TG, 1>(a, p.nv, p.ch, st);
+}
+
 template <typename TR, typename TT, int VEC>
 static void launch_delta(int64_t R, int width, int64_t D, int nv, int ch, const void *rows, const float *weights,
                          const float *prediction, const void *target, const float *beta, const float *log_decay,
@@ -214,6 +301,35 @@ extern "C" int glsdm_proposal_error(int64_t R, int64_t D, const float *predictio
         else launch_error<bf16_t, 1>(R, D, p.nv, p.ch, prediction, target, beta, log_decay, error, decay, st);
     }
     return check_launch("proposal_error_kernel");
+}
+
+extern "C" int glsdm_proposal_append(const int64_t *index, const float *weights, const float *prediction,
+                                     const void *target, int32_t target_dtype, const void *beta_in,
+                                     const void *decay_in, int32_t gate_dtype, int64_t B, int64_t T, int64_t H,
+                                     int32_t width, int64_t S, int64_t D, int64_t position_offset, int64_t chunk,
+                                     int64_t layers, int64_t layer, int64_t *addresses, int64_t *keys,
+                                     float *weights_out, float *error, float *decay, void *stream)
+{
+    if (B < 0 || T < 0 || H < 1 || width < 1 || S < 1 || chunk < 1 || layers < 1 || layer < 0 ||
+        layer >= layers || position_offset < 0)
+        return fail(GLSDM_ERR_ARG, "proposal_append: bad arguments");
+    const int64_t R = B * T * H;
+    int rc = check_proposal_shape("proposal_append", R, D);
+    if (rc) return rc;
+    if (!dtype_ok(target_dtype) || !dtype_ok(gate_dtype)) return fail(GLSDM_ERR_ARG, "proposal_append: bad dtype");
+    if (R == 0) return GLSDM_OK;
+    if (!index || !weights || !prediction || !target || !beta_in || !decay_in || !addresses || !keys ||
+        !weights_out || !error || !decay)
+        return fail(GLSDM_ERR_ARG, "proposal_append: null pointer");
+    const AppendArgs a{R, T, H, width, S, D, position_offset, chunk * layers, layers, layer, index, weights,
+                       prediction, target, beta_in, decay_in, addresses, keys, weights_out, error, decay};
+    const ProposalPlan p = proposal_plan(D, bits_of(prediction, target, error));
+    const hipStream_t st = as_stream(stream);
+    if (target_dtype == GLSDM_F32 && gate_dtype == GLSDM_F32) launch_append_t<float, float>(a, p, st);
+    else if (target_dtype == GLSDM_F32) launch_append_t<float, bf16_t>(a, p, st);
+    else if (gate_dtype == GLSDM_F32) launch_append_t<bf16_t, float>(a, p, st);
+    else launch_append_t<bf16_t, bf16_t>(a, p, st);
+    return check_launch("proposal_append_kernel");
 }
 
 extern "C" int glsdm_proposal_delta(const void *rows, int32_t rows_dtype, int64_t R, int32_t width, int64_t D,

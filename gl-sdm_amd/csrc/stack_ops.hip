@@ -220,23 +220,20 @@ __global__ __launch_bounds__(256) void rms_norm_cast_kernel(const TI *__restrict
     }
 }
 
-// The write gates of a global layer's proposal (S/layers/global_layer.py:48-49):
-// beta = sigmoid(b) = 1 / (1 + exp(-b)) and log_decay = -softplus(d - 4) with
-// softplus(v) = v above 20, else log1p(exp(v)), from the bf16 or fp32 outputs
-// of the beta and decay projections, in fp32.  One thread per (token, head).
+// The write gates of a global layer's proposal (write_gate_values) from the
+// bf16 or fp32 outputs of the beta and decay projections, in fp32.  One thread
+// per (token, head).
 template <typename TX>
 __global__ __launch_bounds__(256) void write_gates_kernel(const TX *__restrict__ b, const TX *__restrict__ d,
                                                           int64_t n, float *__restrict__ beta,
                                                           float *__restrict__ log_decay)
 {
-#pragma clang fp contract(off)
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float bv = RowIO<TX>::load(b + i);
-    beta[i] = 1.0f / (1.0f + expf(-bv));
-    const float v = RowIO<TX>::load(d + i) - 4.0f;
-    const float sp = v > 20.0f ? v : log1pf(expf(v));
-    log_decay[i] = -sp;
+    float bet, ld;
+    write_gate_values(RowIO<TX>::load(b + i), RowIO<TX>::load(d + i), bet, ld);
+    beta[i] = bet;
+    log_decay[i] = ld;
 }
 
 }  // namespace glsdm

@@ -49,6 +49,8 @@ SIGNATURES = {
     "glsdm_write_gates": ([_P, _P, _I32, _I64, _P, _P, _P], _I32),
     "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),
     "glsdm_proposal_error": ([_I64, _I64, _P, _P, _I32, _P, _P, _P, _P, _P], _I32),
+    "glsdm_proposal_append": ([_P, _P, _P, _P, _I32, _P, _P, _I32, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64,
+                               _I64, _I64, _P, _P, _P, _P, _P, _P], _I32),
     "glsdm_proposal_delta": ([_P, _I32, _I64, _I32, _I64, _P, _P, _P, _I32, _P, _P, _P, _I64, _P, _P], _I32),
     "glsdm_route_backward": ([_P, _P, _P, _I64, _I32, _I32, _P, _P], _I32),
     "glsdm_read_backward_weights": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _P], _I32),

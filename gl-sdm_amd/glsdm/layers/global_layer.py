@@ -7,7 +7,7 @@ import torch.nn.functional as F
 
 from .. import _native as N
 from ..memory import routing
-from ..memory.proposals import layer_proposal
+from ..memory.proposals import layer_proposal, log_proposal
 from .block import check_reg_mode, regulariser, zero
 from .common import MLP, RMSNorm
 from .router import GlobalRouter
@@ -48,7 +48,7 @@ class GlobalLayer(nn.Module):
         x = x + self.mlp(self.norm2.cast(x, dtype))
         return x, regulariser(x, self.reg_mode), zero(x)
 
-    def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None):
+    def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None, log=None):
         """Write proposal of the chunk's tokens against ``snapshot``.
 
         Each token-head's delta against the rows its write route picks is
@@ -56,9 +56,11 @@ class GlobalLayer(nn.Module):
         mass 1, with no averaging over tokens or layers; collisions commit in
         (address, position in chunk, layer) order through the keys.  Outside
         autograd the deltas stay deferred: the commit forms them from the rows
-        it touches.  Under autograd (training with writes) they are
-        materialised as the reference does, so gradients flow through the
-        commit into later chunks' reads.
+        it touches; with a proposal ``log`` (the stack's inference path) the
+        gates, keys and error terms go straight into the log in one launch.
+        Under autograd (training with writes) they are materialised as the
+        reference does, so gradients flow through the commit into later
+        chunks' reads.
         """
         training = torch.is_grad_enabled() and (x.requires_grad or snapshot.values.requires_grad)
         B, T, _ = x.shape
@@ -70,6 +72,9 @@ class GlobalLayer(nn.Module):
         dense = zk if vdt == zk.dtype else self.norm1.cast(x, vdt)
         target = router.v(dense).view(B, T, router.heads, router.head_dim)
         b_lin, d_lin = router.beta(dense), router.decay(dense)
+        if log is not None and not training and b_lin.is_cuda and b_lin.dtype in (torch.float32, torch.bfloat16):
+            return log_proposal(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx,
+                                chunk_size, num_layers)
         if training or not b_lin.is_cuda or b_lin.dtype not in (torch.float32, torch.bfloat16):
             beta = b_lin.float().sigmoid().unsqueeze(-1)
             log_decay = -F.softplus(d_lin.float() - 4).unsqueeze(-1)

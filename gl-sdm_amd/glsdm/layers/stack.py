@@ -11,11 +11,16 @@ prefill/decode calls.  The last chunk of a stateless call proposes nothing.
 Outside autograd the commit updates the cache's own snapshot storage in place
 (``gl_commit_in_place``, default on): the snapshot of a chunk is dropped at
 its commit anyway, and a full-bank copy per commit is the cost the fused
-commit exists to avoid.
+commit exists to avoid.  Outside autograd the global layers also append
+their proposals to the cache's proposal log (``gl_proposal_log``, default
+on): one chunk of preallocated device rows that the commit reads as one
+proposal, so a decode chunk's thousands of one-token proposals are never
+concatenated.
 """
 import torch
 
-from ..memory import commit, merge
+from ..memory import LoggedProposal, commit, merge
+from ..memory.proposals import ProposalLog
 from .block import Block, zero
 from .global_layer import GlobalLayer
 
@@ -36,6 +41,19 @@ def make_layers(cfg):
     return [GlobalLayer(cfg) if pattern[i % len(pattern)] == "global" else Block(local, i) for i in range(count)]
 
 
+def _proposal_log(model, cache, batch, chunk):
+    """The cache's proposal log, sized for one chunk of every global layer's
+    proposals (a new one when the cache has none, or none of this shape)."""
+    layers = [b for b in model.blocks if isinstance(b, GlobalLayer)]
+    router = layers[0].attn
+    H, k, D = router.heads, router.num_writes, cache.view.values.shape[-1]
+    rows = len(layers) * chunk * batch * H
+    device = cache.view.values.device
+    if cache.log is None or (not cache.pending and not cache.log.fits(rows, H, k, D, device)):
+        cache.log = ProposalLog(rows, H, k, D, device)
+    return cache.log
+
+
 def forward(model, inputs, cache=None):
     """Run embedded ``inputs [B, T, dim]`` through the stack; returns
     ``(hidden [B, T, dim], reg, align)``.  ``cache`` is a request cache
@@ -49,6 +67,10 @@ def forward(model, inputs, cache=None):
     C = model.cfg.get("gl_chunk_size", 512)
     layers = len(model.blocks)
     in_place = model.cfg.get("gl_commit_in_place", True) and not torch.is_grad_enabled()
+    # proposal log: inference on the device, and no pending proposal of another kind
+    use_log = (model.cfg.get("gl_proposal_log", True) and not torch.is_grad_enabled() and cache.view.values.is_cuda
+               and any(isinstance(b, GlobalLayer) for b in model.blocks)
+               and all(isinstance(p, LoggedProposal) for p in cache.pending))
     outputs = []
     reg, align = inputs.new_zeros(()), inputs.new_zeros(())
     position = 0
@@ -58,12 +80,13 @@ def forward(model, inputs, cache=None):
         snapshot = cache.view
         writes = retain or position + length < T
         proposals = list(cache.pending)
+        log = _proposal_log(model, cache, B, C) if use_log and writes else None
         x = inputs[:, position:position + length]
         for i, block in enumerate(model.blocks):
             if isinstance(block, GlobalLayer):
                 x, r, a = block(x, snapshot)
                 if writes:
-                    proposals.append(block.propose(x, snapshot, offset, i, C, layers))
+                    proposals.append(block.propose(x, snapshot, offset, i, C, layers, log=log))
             else:
                 x, r, a = block(x, cache.local.setdefault(i, {}))
             if r is not zero(r) or a is not zero(a):     # the baseline's are the shared zeros: nothing to add
@@ -72,6 +95,8 @@ def forward(model, inputs, cache=None):
         if cache.tokens % C == 0 and writes:
             cache.view = commit(snapshot, merge(snapshot, proposals), donate=in_place)
             cache.pending = ()
+            if cache.log is not None:
+                cache.log.clear()          # its rows are committed: the next chunk reuses them
         else:
             cache.pending = tuple(proposals)
         outputs.append(x)

@@ -68,6 +68,34 @@ class DeferredProposal:
 
 
 @dataclass(frozen=True)
+class LoggedProposal:
+    """A deferred write proposal stored in a proposal log (``ProposalLog``):
+    rows ``[start, start + rows)`` of the log hold its addresses, collision
+    keys and route weights (``width`` per row) and its per-row error and decay
+    terms, written when it was made.  ``generation`` is the log's generation
+    at that time: the log's rows are reused after each commit, and a proposal
+    of an earlier generation no longer has its rows."""
+    base_version: int
+    lineage: object
+    log: object
+    generation: int
+    start: int
+    rows: int
+
+    @property
+    def heads(self):
+        return self.log.heads
+
+    @property
+    def width(self):
+        return self.log.width
+
+    @property
+    def sort_keys(self):
+        return self.log.keys.narrow(0, self.start * self.log.width, self.rows * self.log.width)
+
+
+@dataclass(frozen=True)
 class WriteBuffer:
     base_version: int
     proposals: tuple
@@ -81,6 +109,7 @@ class MemoryCache:
     tokens: int = 0
     pending: tuple = ()
     local: dict = field(default_factory=dict)
+    log: object = None      # the stack's ProposalLog for the pending chunk (inference)
 
 
 class MemoryBank(nn.Module):

@@ -8,8 +8,9 @@ place instead of returning a new bank (the old view must not be used again).
 """
 import torch
 
-from .state import DeferredProposal, MemoryView, WriteBuffer
+from .state import DeferredProposal, LoggedProposal, MemoryView, WriteBuffer
 from .backends import hip
+from .proposals import _ones
 
 BACKENDS = ("hip",)
 
@@ -59,11 +60,40 @@ def _commit_deferred(view, props, keys, donate):
                                 weights.contiguous(), error, decay, mass.contiguous(), donate=donate)
 
 
+def _commit_logged(view, props, donate):
+    """Proposals of one proposal log: one fused commit of their rows.  When they
+    are the log's rows in order from its start (the stack's chunk), the log's
+    buffers are committed as they lie; else their rows are gathered in the
+    buffer's order (which breaks ties of equal keys, as concatenation does)."""
+    log = props[0].log
+    if any(p.log is not log for p in props):
+        raise ValueError("logged proposals commit only with proposals of the same log")
+    if any(p.generation != log.generation for p in props):
+        raise ValueError("stale proposal: its log's rows were reused after a commit")
+    in_order, at = True, 0
+    for p in props:
+        in_order &= p.start == at
+        at += p.rows
+    if in_order:
+        terms = log.terms(0, at)
+    else:
+        parts = [log.terms(p.start, p.rows) for p in props]
+        terms = tuple(torch.cat(t) for t in zip(*parts))
+    addresses, keys, weights, error, decay = terms
+    mass = _ones(addresses.shape[:1], addresses.device)
+    return hip.commit_proposals(view.values, addresses, keys, weights, error, decay, mass, donate=donate)
+
+
 def commit(view, buffer, reference=False, backend="hip", donate=False):
     _check_backend(backend, reference)
     if buffer.base_version != view.version or buffer.lineage is not view.lineage:
         raise ValueError("stale memory transaction")
     props = buffer.proposals
+    logged = [isinstance(p, LoggedProposal) for p in props]
+    if any(logged):
+        if not all(logged):
+            raise ValueError("logged proposals commit only with proposals of the same log")
+        return MemoryView(_commit_logged(view, props, donate), view.version + 1, view.lineage)
     keyed = [p.sort_keys is not None for p in props]
     if any(keyed) and not all(keyed):
         raise ValueError("cannot mix keyed and unkeyed proposals")

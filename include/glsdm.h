@@ -302,6 +302,32 @@ int glsdm_proposal_error(int64_t R, int64_t D, const float *prediction, const vo
                          float *error, float *decay, void *stream);
 
 /*
+ * One write proposal appended to a proposal log (preallocated per-chunk
+ * buffers that the fused commit later reads as one proposal), for the
+ * B*T*H proposal rows r = (b*T + t)*H + h of a [B, T, H, width] write route:
+ *   error [R, D] fp32, decay [R] fp32:   glsdm_proposal_error of the row, with
+ *       beta = sigmoid(b) = 1 / (1 + exp(-b)) and log_decay = -softplus(d - 4)
+ *       (softplus(v) = v above 20, else log1p(exp(v))) from beta_in / decay_in
+ *       [R] (the beta and decay projections' outputs, of gate_dtype);
+ *   addresses, keys [R*width] int64:    glsdm_proposal_keys of index;
+ *   weights_out [R*width] fp32:         a copy of the route weights.
+ * The output pointers are the log's buffers at its current fill; index
+ * [B,T,H,width] int64, weights the same shape fp32, prediction [R, D] fp32,
+ * target [R, D] of target_dtype.  Bitwise equal to write gates +
+ * glsdm_proposal_keys + glsdm_proposal_error.
+ * Replaces: the proposal construction of S/layers/global_layer.py:45-54 (gates
+ * :48-49, keys :52-53) and the per-row terms of S/runtime/dense.py:12-13; the
+ * list of proposals the reference concatenates at its commit
+ * (S/memory/transactions.py:73-79) becomes the log's buffers.
+ */
+int glsdm_proposal_append(const int64_t *index, const float *weights, const float *prediction,
+                          const void *target, int32_t target_dtype, const void *beta_in, const void *decay_in,
+                          int32_t gate_dtype, int64_t B, int64_t T, int64_t H, int32_t width, int64_t S,
+                          int64_t D, int64_t position_offset, int64_t chunk, int64_t layers, int64_t layer,
+                          int64_t *addresses, int64_t *keys, float *weights_out, float *error, float *decay,
+                          void *stream);
+
+/*
  * Materialised write-proposal deltas, for R proposal rows of `width` entries:
  *   deltas[r, j, :] = mass[r / heads] * ((decay[r] - 1) * rows[r, j, :]
  *                                        + weights[r, j] * error[r, :])

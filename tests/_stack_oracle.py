@@ -15,6 +15,7 @@ from types import SimpleNamespace
 from unittest.mock import patch
 
 import torch
+import torch.nn.functional as F
 
 from oracle import torch_oracle
 from glsdm.layers import global_layer, stack
@@ -59,6 +60,21 @@ def _layer_proposal(snapshot, index, weights, prediction, target, beta, log_deca
     return WriteProposal(snapshot.version, addresses.flatten(), delta.flatten(0, 3), snapshot.lineage, keys.flatten())
 
 
+def _gates(b_lin, d_lin):
+    # the reference's write gates (S/layers/global_layer.py:48-49), on the host
+    beta = b_lin.cpu().float().sigmoid().unsqueeze(-1)
+    log_decay = -F.softplus(d_lin.cpu().float() - 4).unsqueeze(-1)
+    return beta, log_decay
+
+
+def _log_proposal(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx, chunk_size,
+                  num_layers):
+    del log
+    beta, log_decay = _gates(b_lin, d_lin)
+    return _layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx,
+                           chunk_size, num_layers)
+
+
 def _commit(view, buffer, reference=False, backend="hip", donate=False):
     del reference, backend, donate
     values = view.values
@@ -77,6 +93,7 @@ def oracle_memory():
     _HOST[:] = [None, None]
     with patch.object(routing, "routed_read", _routed_read), \
             patch.object(global_layer, "layer_proposal", _layer_proposal), \
+            patch.object(global_layer, "log_proposal", _log_proposal), \
             patch.object(stack, "commit", _commit):
         yield
 
@@ -115,6 +132,7 @@ class Shadow:
     @contextlib.contextmanager
     def watch(self):
         native_read, native_propose, native_commit = routing.routed_read, global_layer.layer_proposal, stack.commit
+        native_log = global_layer.log_proposal
 
         def read(block, memory, scores, width, physical=None):
             out, index, weights = native_read(block, memory, scores, width, physical)
@@ -138,6 +156,18 @@ class Shadow:
             self.proposals += 1
             return p
 
+        def log_propose(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx,
+                        chunk_size, num_layers):
+            p = native_log(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx,
+                           chunk_size, num_layers)
+            host = SimpleNamespace(values=self._host(snapshot.values), version=snapshot.version,
+                                   lineage=snapshot.lineage)
+            beta, log_decay = _gates(b_lin, d_lin)
+            self._refs[id(p)] = (p, _layer_proposal(host, index, weights, prediction, target, beta, log_decay,
+                                                    offset, layer_idx, chunk_size, num_layers))
+            self.proposals += 1
+            return p
+
         def commit(view, buffer, reference=False, backend="hip", donate=False):
             refs = [self._refs.pop(id(p))[1] for p in buffer.proposals]
             values = view.values
@@ -156,7 +186,7 @@ class Shadow:
             return new
 
         with patch.object(routing, "routed_read", read), patch.object(global_layer, "layer_proposal", propose), \
-                patch.object(stack, "commit", commit):
+                patch.object(global_layer, "log_proposal", log_propose), patch.object(stack, "commit", commit):
             yield self
 
 

@@ -155,3 +155,11 @@ def test_stack_ops_reject_bad_arguments_before_launch():
     assert _rc("glsdm_rms_norm_cast", one, 1, one, 0, 4, 0, eps, one, 1, None) == N.ERR_ARG       # dim 0
     assert _rc("glsdm_write_gates", one, one, 1, -1, one, one, None) == N.ERR_ARG
     assert _rc("glsdm_write_gates", None, None, 1, 0, None, None, None) == N.OK                 # empty
+    # proposal_append(index, weights, prediction, target, tdtype, beta, decay, gdtype, B, T, H, width, S, D,
+    #                 offset, chunk, layers, layer, addresses, keys, weights_out, error, decay_out, stream)
+    append = lambda T, D, layer, gdtype: _rc("glsdm_proposal_append", one, one, one, one, 1, one, one, gdtype, 2, T,
+                                             4, 8, 64, D, 0, 4, 2, layer, one, one, one, one, one, None)
+    assert append(1, 64, 2, 1) == N.ERR_ARG                # layer >= layers
+    assert append(1, 4096, 0, 1) == N.ERR_UNSUPPORTED      # D above 2048
+    assert append(1, 64, 0, 7) == N.ERR_ARG                # gate dtype
+    assert append(0, 64, 0, 1) == N.OK                     # empty
