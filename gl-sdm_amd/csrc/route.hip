@@ -232,6 +232,15 @@ static int launch_route(const TS *scores, int64_t rows, int half, int width, int
         // candidate and output stages keep the single kernel's G-lane groups, whose
         // softmax summation order fixes the bits
         constexpr int MG = G > 16 ? G : 16;
+        if constexpr (K == 16 || K == 32) {
+            if ((int64_t)half * half <= (1ll << 30)) {
+                // one wavefront per row (the same bits as route_merge_kernel<K, G, MG>)
+                hipLaunchKernelGGL((route_merge_wave_kernel<K, G, 8>), dim3((unsigned)ceil_div(rows, 4)), dim3(256),
+                                   0, st, parts, rows, sp.splits, half, width, tie, index, weights, KeyArgs{},
+                                   (int64_t)1);
+                return check_launch("route_merge_wave_kernel");
+            }
+        }
         hipLaunchKernelGGL((route_merge_kernel<K, G, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0,
                            st, parts, rows, sp.splits, half, width, tie, index, weights, KeyArgs{}, (int64_t)1);
         return check_launch("route_merge_kernel");

@@ -379,6 +379,14 @@ static int launch_split(const void *q, const void *keys, int64_t N, int64_t H, i
     if (rc) return rc;
     constexpr int MG = K >= 32 ? 8 : 4;
     const int64_t rows = N * H;
+    if constexpr (K == 16 || K == 32) {
+        if ((int64_t)half * half <= (1ll << 30)) {
+            // one wavefront per row (the same bits as route_merge_kernel<K, MG>)
+            hipLaunchKernelGGL((route_merge_wave_kernel<K, MG, 8>), dim3((unsigned)ceil_div(rows, 4)), dim3(256), 0,
+                               st, parts, rows, p.splits, half, width, tie, index, weights, ka, H);
+            return check_launch("route_merge_wave_kernel");
+        }
+    }
     hipLaunchKernelGGL((route_merge_kernel<K, MG>), dim3((unsigned)ceil_div(rows, 256 / MG)), dim3(256), 0, st,
                        parts, rows, p.splits, half, width, tie, index, weights, ka, H);
     return check_launch("route_merge_kernel");

@@ -356,24 +356,35 @@ __device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], cons
                                              const KeyRow &kr)
 {
     uint32_t slot[K];
+    float val[K];
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < K; ++w) {
         slot[w] = w < width ? ck.slot(t[w]) : 0xFFFFFFFFu;
-        if (w < width) {
-            const float s = order_value(ck.order(t[w]));
-            m = (s > m || s != s) ? s : m;
-        }
+        val[w] = order_value(ck.order(t[w]));
+        if (w < width) m = (val[w] > m || val[w] != val[w]) ? val[w] : m;
     }
     constexpr int MINE = (K + G - 1) / G;
+    // this lane's picks w = u*G + g, selected from the G candidates of each u
+    // (register selects: a lane-dependent index would put the lists in scratch)
     float e[MINE];
+    uint32_t my_slot[MINE];
     float part = 0.0f;
 #pragma unroll
     for (int u = 0; u < MINE; ++u) {
+        float x = 0.0f;
+        my_slot[u] = 0xFFFFFFFFu;
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+            if (u * G + q < K && q == g) {
+                x = val[u * G + q];
+                my_slot[u] = slot[u * G + q];
+            }
+        }
         const int w = u * G + g;
         e[u] = 0.0f;
         if (w < width && w < K) {
-            e[u] = expf(order_value(ck.order(t[w])) - m);
+            e[u] = expf(x - m);
             part += e[u];
         }
     }
@@ -388,11 +399,11 @@ __device__ __forceinline__ void finish_route(const typename CK::KT (&t)[K], cons
             if (w < width && w < K) {
                 int rank = 0;
 #pragma unroll
-                for (int j = 0; j < K; ++j) rank += slot[j] < slot[w] ? 1 : 0;
-                index_row[rank] = (int64_t)slot[w];
+                for (int j = 0; j < K; ++j) rank += slot[j] < my_slot[u] ? 1 : 0;
+                index_row[rank] = (int64_t)my_slot[u];
                 weight_row[rank] = e[u] * inv;
                 if (kr.addr) {
-                    const int64_t a = kr.base + (int64_t)slot[w];
+                    const int64_t a = kr.base + (int64_t)my_slot[u];
                     kr.addr[rank] = a;
                     kr.keys[rank] = a * kr.mul + kr.add;
                 }
@@ -567,6 +578,235 @@ __global__ __launch_bounds__(256) void route_merge_kernel(const uint64_t *__rest
     const KeyRow kr = ka.addr ? key_row(ka, r, heads, width) : KeyRow{nullptr, nullptr, 0, 0, 0};
     route_tail<K, G>(s_idx[lr][0], s_val[lr][0], s_idx[lr][1], s_val[lr][1], half, width, tie, g, s_pairs, npairs,
                      finite, live && m < G, index + r * width, weights + r * width, kr);
+}
+
+// ------------------------------------------------------------ wave-per-row merge
+//
+// Sorting networks over keys held E per lane, blocked across a wavefront:
+// element i lives in lane i / E, register i % E.  Cross-lane steps exchange
+// whole registers with lane ^ (stride / E).
+
+// One compare-exchange step over elements i and i ^ STRIDE: the lower index
+// keeps the larger key where desc(i) holds, the smaller one elsewhere.
+template <int E, int STRIDE, typename KT, typename DescFn>
+__device__ __forceinline__ void wave_cx(KT (&v)[E], int lane, DescFn desc)
+{
+    if constexpr (STRIDE >= E) {
+        constexpr int M = STRIDE / E;
+        const bool upper = (lane & M) != 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const KT x = lane_xor<M>(v[e]);
+            v[e] = (desc(lane * E + e) != upper) ? kmax(v[e], x) : kmin(v[e], x);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int f = e ^ STRIDE;
+            if (f > e) {
+                const KT a = v[e], b = v[f];
+                const bool d = desc(lane * E + e);
+                v[e] = d ? kmax(a, b) : kmin(a, b);
+                v[f] = d ? kmin(a, b) : kmax(a, b);
+            }
+        }
+    }
+}
+
+template <int E, int SIZE, int STRIDE, typename KT>
+__device__ __forceinline__ void wave_sort_stage(KT (&v)[E], int lane)
+{
+    wave_cx<E, STRIDE>(v, lane, [](int i) { return (i & SIZE) == 0; });
+    if constexpr (STRIDE > 1) wave_sort_stage<E, SIZE, STRIDE / 2>(v, lane);
+}
+
+template <int E, int SIZE, typename KT>
+__device__ __forceinline__ void wave_sort_from(KT (&v)[E], int lane)
+{
+    wave_sort_stage<E, SIZE, SIZE / 2>(v, lane);
+    if constexpr (SIZE < 64 * E) wave_sort_from<E, SIZE * 2>(v, lane);
+}
+
+// Bitonic sort of the wavefront's 64*E keys, descending (element 0 the largest).
+template <int E, typename KT>
+__device__ __forceinline__ void wave_sort_desc(KT (&v)[E], int lane)
+{
+    wave_sort_from<E, 2>(v, lane);
+}
+
+// Half-cleaner of a bitonic sequence of K keys held E per lane in segments of
+// K / E lanes: afterwards each segment's list is sorted descending.
+template <int E, int S, typename KT>
+__device__ __forceinline__ void seg_clean(KT (&v)[E], int lane)
+{
+    wave_cx<E, S>(v, lane, [](int) { return true; });
+    if constexpr (S > 1) seg_clean<E, S / 2>(v, lane);
+}
+
+// Lists of K keys sorted descending, one per segment of P = K / E lanes: each
+// segment gets the top K of its own list and that of segment seg ^ M.  The
+// partner list is read reversed (lane pl takes lane P-1-pl's registers in
+// reverse), so the elementwise maximum is bitonic and holds the top K.
+template <int K, int E, int M, typename KT>
+__device__ __forceinline__ void seg_merge(KT (&v)[E], int lane)
+{
+    constexpr int P = K / E;
+    KT x[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = lane_xor<M * P + P - 1>(v[E - 1 - e]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = kmax(v[e], x[e]);
+    seg_clean<E, K / 2>(v, lane);
+}
+
+// Butterfly over the first `used` segments (a power of two) of each half-wave.
+template <int K, int E, int M, typename KT>
+__device__ __forceinline__ void seg_butterfly(KT (&v)[E], int lane, int used)
+{
+    constexpr int NSEG = 32 / (K / E);                // segments per half-wave
+    if constexpr (M < NSEG) {
+        if (M < used) seg_merge<K, E, M>(v, lane);     // wave-uniform
+        seg_butterfly<K, E, 2 * M>(v, lane, used);
+    }
+}
+
+// Wave-per-row variant of route_merge_kernel for the split paths' K = 16 and 32
+// with slots in 30 bits: one wavefront per row, so the merge, the candidate
+// stage and their selections run on 64 lanes instead of one lane group.
+//   merge      half-wave f merges factor f: segment s (P = K / E lanes) loads
+//              range lists s, s + NSEG, ... (folded in), then a butterfly of
+//              bitonic merges leaves the factor's top K in every segment
+//   candidates the staircase cells (E2 per lane) are keyed as CellKeyD and
+//              sorted across the wave; the same verification as
+//              candidate_top, else the whole kk x kk grid (E3 per lane)
+//   output     the sorted top-K through LDS into finish_route's G-lane group,
+//              so the slots, the softmax and its summation order are those of
+//              route_merge_kernel<K, G> bit for bit.
+template <int K, int G, int E>
+__global__ __launch_bounds__(256) void route_merge_wave_kernel(const uint64_t *__restrict__ parts, int64_t rows,
+                                                               int splits, int half, int width, int tie,
+                                                               int64_t *__restrict__ index,
+                                                               float *__restrict__ weights, KeyArgs ka,
+                                                               int64_t heads)
+{
+    static_assert(K % E == 0 && (K == 16 || K == 32) && K * K % 64 == 0, "wave merge shape");
+    constexpr int P = K / E, NSEG = 32 / P;
+    constexpr int E2 = K == 16 ? 1 : 2;               // staircase of width <= K: at most 50 / 119 cells
+    constexpr int E3 = K * K / 64;                    // the whole kk x kk grid, kk <= K
+    __shared__ uint32_t s_idx[4][2][K];
+    __shared__ float s_val[4][2][K];
+    __shared__ double s_t[4][K];
+    __shared__ uint16_t s_pairs[STAIR_MAX];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wv;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;
+    const int kk = width < half ? width : half;
+    const int npairs = staircase_build(s_pairs, kk, width);
+
+    // 1. factor lists: half-wave f, segment seg, lane pl of the segment
+    const int f = lane >> 5, seg = (lane & 31) / P, pl = lane % P;
+    double v[E];
+    const uint64_t *base = parts + (r * 2 + f) * splits * (int64_t)K;
+    if (seg < splits) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = narrow_keyd(base[(int64_t)seg * K + pl * E + e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = 0.0;
+    }
+    // more range lists than segments: each segment folds in lists seg + NSEG, ...
+    // (read reversed; a segment without one takes empty keys, which keep its
+    // list as it is), every lane in every round since the clean crosses lanes
+    for (int s0 = NSEG; s0 < splits; s0 += NSEG) {
+        const int s = s0 + seg;
+        const uint64_t *src = base + (int64_t)s * K;
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = kmax(v[e], s < splits ? narrow_keyd(src[K - 1 - (pl * E + e)]) : 0.0);
+        seg_clean<E, K / 2>(v, lane);
+    }
+    int used = 1;                                     // segments holding lists, to a power of two
+    while (used < splits && used < NSEG) used <<= 1;
+    seg_butterfly<K, E, 1>(v, lane, used);
+    bool ok = true;
+    if (seg == 0) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = pl * E + e;
+            if (i < kk) {
+                const float x = key_value(v[e]);
+                ok = ok && (fabsf(x) <= 3.402823466e38f);
+                s_idx[wv][f][i] = key_index(v[e], tie);
+                s_val[wv][f][i] = x;
+            }
+        }
+    }
+    const bool finite = __ballot(!ok) == 0;
+    __syncthreads();                                  // stashed lists and the staircase cells
+
+    // 2. candidate stage
+    const uint32_t *i0 = s_idx[wv][0], *i1 = s_idx[wv][1];
+    const float *v0 = s_val[wv][0], *v1 = s_val[wv][1];
+    int ib = 1;
+    while ((1ll << ib) < (int64_t)half * half) ++ib;
+    const CellKeyD ck{tie, ib, 30 - ib, (uint32_t)((1ull << ib) - 1ull)};
+    auto cell = [&](int i, int j) { return ck.make(v0[i] + v1[j], i0[i] * (uint32_t)half + i1[j]); };
+    bool exact = false;
+    if (finite && npairs >= width) {
+        double c[E2];
+#pragma unroll
+        for (int e = 0; e < E2; ++e) {
+            const int q = lane * E2 + e;
+            c[e] = 0.0;
+            if (q < npairs) {
+                const int pr = s_pairs[q];
+                c[e] = cell(pr >> 8, pr & 0xFF);
+            }
+        }
+        wave_sort_desc<E2>(c, lane);
+        // verify: the first excluded cell of each grid row scores strictly below the width-th pick
+        double wth = 0.0;
+#pragma unroll
+        for (int e = 0; e < E2; ++e)
+            if (lane * E2 + e == width - 1) wth = c[e];
+        wth = __shfl(wth, (width - 1) / E2);
+        const uint32_t tau = ck.order(wth);
+        bool good = true;
+        if (lane < kk) {
+            const int j = min(kk, width / (lane + 1));
+            if (j < kk) good = order_bits(v0[lane] + v1[j]) < tau;
+        }
+        exact = __ballot(!good) == 0;
+        if (exact) {
+#pragma unroll
+            for (int e = 0; e < E2; ++e)
+                if (lane * E2 + e < K) s_t[wv][lane * E2 + e] = c[e];
+        }
+    }
+    if (!exact) {                                     // wave-uniform
+        double c[E3];
+#pragma unroll
+        for (int e = 0; e < E3; ++e) {
+            const int q = lane * E3 + e;
+            c[e] = 0.0;
+            if (q < kk * kk) {
+                const int i = q / kk;
+                c[e] = cell(i, q - i * kk);
+            }
+        }
+        wave_sort_desc<E3>(c, lane);
+#pragma unroll
+        for (int e = 0; e < E3; ++e)
+            if (lane * E3 + e < K) s_t[wv][lane * E3 + e] = c[e];
+    }
+    __syncthreads();
+
+    // 3. output: every lane holds the list; the first G lanes write the row
+    double t[K];
+#pragma unroll
+    for (int w = 0; w < K; ++w) t[w] = s_t[wv][w];
+    const KeyRow kr = ka.addr ? key_row(ka, r, heads, width) : KeyRow{nullptr, nullptr, 0, 0, 0};
+    finish_route<K, G>(t, ck, width, lane % G, live && lane < G, index + r * width, weights + r * width, kr);
 }
 
 }  // namespace glsdm
