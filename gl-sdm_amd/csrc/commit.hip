@@ -324,15 +324,22 @@ __global__ __launch_bounds__(SORT_THREADS) void onesweep_kernel(const uint64_t *
 // bucket path, two launches): the words are grouped by their top address digit
 // (256 buckets, stable) and one block per bucket sorts its words by the
 // remaining address digits, least significant first, each pass stable, so the
-// result equals the full LSD sort.  A bucket of up to BK_CAP words is sorted
+// result equals the full LSD sort.  The top digit is taken from the bits of the
+// largest real row (rows - 1), so real rows spread over all 256 buckets; the
+// out-of-range value `rows` clamps to the last bucket when rows is a power of
+// two, and that bucket's sort then also covers the sentinel's bit (one more
+// pass), which orders it after every real row.  A bucket of up to BK_CAP words is sorted
 // in LDS; a larger one (skewed addresses) in chunks of BK_CAP through global
 // scratch, with a counting pass per digit.
 #ifndef GLSDM_BK_THREADS
 #define GLSDM_BK_THREADS 1024
 #endif
 constexpr int BK_THREADS = GLSDM_BK_THREADS;
-constexpr int BK_ITEMS = 8192 / BK_THREADS;
-constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // 8192 words
+#ifndef GLSDM_BK_CAP
+#define GLSDM_BK_CAP 8192
+#endif
+constexpr int BK_ITEMS = GLSDM_BK_CAP / BK_THREADS;
+constexpr int BK_CAP = BK_THREADS * BK_ITEMS;          // words a bucket may hold to be sorted in LDS
 constexpr int BK_WAVES = BK_THREADS / 64;
 
 // Stable ranks of one chunk's items (held BK_ITEMS per thread at wave-major
@@ -418,7 +425,8 @@ __global__ __launch_bounds__(BT_THREADS) void tile_bucket_kernel(const int64_t *
         const int64_t a = valid ? addresses[i] : 0;
         const uint64_t row = (a >= 0 && a < rows) ? (uint64_t)a : (uint64_t)rows;   // out of range: one run, dropped
         v[k] = (row << ebits) | (uint64_t)i;
-        const uint32_t d = (uint32_t)(v[k] >> shift) & (RADIX - 1);
+        const uint64_t top = v[k] >> shift;                        // <= RADIX: the clamped sentinel
+        const uint32_t d = top < (uint64_t)RADIX ? (uint32_t)top : (uint32_t)(RADIX - 1);
         dig[k] = d;
         uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -502,8 +510,10 @@ __global__ __launch_bounds__(BK_THREADS) void bucket_sort_kernel(const uint64_t 
                                                                       int64_t tiles, int64_t n,
                                                                       uint64_t *__restrict__ scratch,
                                                                       uint64_t *__restrict__ out, int ebits,
-                                                                      int lpasses, uint32_t *__restrict__ error)
+                                                                      int lpasses_all, int lpasses_last,
+                                                                      uint32_t *__restrict__ error)
 {
+    const int lpasses = blockIdx.x == RADIX - 1 ? lpasses_last : lpasses_all;
     __shared__ uint64_t s_x[BK_CAP];
     __shared__ uint64_t s_y[BK_CAP];
     __shared__ uint32_t cnt[BK_WAVES][RADIX];
@@ -980,8 +990,8 @@ __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t
         }
         if (in_order) {
             // PF entries' delta pieces are fetched before they are added (in order),
-            // so a long run is not one load latency per entry
-            constexpr int PF = CH * VEC >= 64 ? 1 : 64 / (CH * VEC);
+            // so a long run costs one load latency per PF entries, not per entry
+            constexpr int PF = CH * VEC >= 64 ? 1 : (CH * VEC >= 32 ? 2 : 128 / (CH * VEC));
             for (int q0 = 0; q0 < len; q0 += lpr) {
                 const int q = q0 + li;
                 const int my_ent = q < len ? (int)(sorted[hp + q] & emask) : (int)n;
@@ -1192,13 +1202,17 @@ static int commit_sort(int64_t rows, const int64_t *addresses, int64_t entries, 
     if (passes >= 3) {
         // each tile orders its words by the top address digit (-> b, pieces in the
         // look-back words' space), then each bucket gathers its pieces and sorts them (-> c)
-        const int msd = ebits + abits - RADIX_BITS;
+        // top digit: bits [real - 8, real) of the address, real = the bits of rows - 1
+        const int real = address_bits(rows - 1);
+        const int msd = ebits + real - RADIX_BITS;
+        const int lpasses = (real - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS;
+        const bool pow2 = (rows & (rows - 1)) == 0;      // the sentinel `rows` clamps into the last bucket
+        const int last = pow2 ? (real + 1 + RADIX_BITS - 1) / RADIX_BITS : lpasses;
         hipLaunchKernelGGL(tile_bucket_kernel, dim3((unsigned)ws.bucket_tiles), dim3(BT_THREADS), 0, st, addresses,
                            rows, ebits, msd, entries, ws.b, ws.status, ws.bucket_tiles, ws.counter);
         if ((rc = check_launch("tile_bucket_kernel"))) return rc;
         hipLaunchKernelGGL(bucket_sort_kernel, dim3(RADIX), dim3(BK_THREADS), 0, st, ws.b, ws.status, ws.bucket_tiles,
-                           entries, ws.a, ws.c, ebits, (abits - RADIX_BITS + RADIX_BITS - 1) / RADIX_BITS,
-                           ws.counter + CW_ERROR);
+                           entries, ws.a, ws.c, ebits, lpasses, last, ws.counter + CW_ERROR);
         if ((rc = check_launch("bucket_sort_kernel"))) return rc;
         sort_result(ws, passes, sorted, long_runs);
         *ebits_out = ebits;

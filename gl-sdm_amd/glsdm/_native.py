@@ -10,7 +10,8 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libglsdm.so")
+# the in-tree build; GLSDM_LIB names another build of the same library
+LIB_PATH = os.environ.get("GLSDM_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libglsdm.so")
 
 F32, BF16 = 0, 1
 TIE_HIGHEST, TIE_LOWEST = 0, 1
