@@ -127,7 +127,8 @@ class Pipeline:
       next to the step time come from a separate serial pass.
     """
 
-    def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False, split_commit=False):
+    def __init__(self, cfg, device, write_path="deltas", backward=False, overlay=False, split_commit=False,
+                 route_parts=0):
         from glsdm import _native as N
         self.N, self.cfg, self.dev, self.write_path, self.backward = N, cfg, device, write_path, backward
         self.overlay = overlay
@@ -191,6 +192,17 @@ class Pipeline:
             self.bw_ws = torch.empty(size.value, dtype=torch.uint8, device=device)
         self.mem_stream = torch.cuda.current_stream(device)
         self.route_stream = torch.cuda.Stream(device)          # default priority
+        # overlap schedule: each route call in `route_parts` launches over consecutive
+        # request ranges, so at most about one fused-route block per CU runs beside the
+        # memory stream's kernels (more leave them too few registers; measured)
+        # (auto: the synthetic-delta write path; the proposal paths' longer memory stream
+        # runs better beside whole launches, measured)
+        tiles = -(-B * C // 64) * H
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        parts = route_parts or (max(1, tiles // cus) if write_path == "deltas" else 1)
+        while parts > 1 and B % parts:
+            parts -= 1
+        self.route_parts = parts
         self.routed = [torch.cuda.Event() for _ in range(self.epochs)]
         self.consumed = [torch.cuda.Event() for _ in range(self.epochs)]
         for ev in self.consumed:
@@ -208,6 +220,8 @@ class Pipeline:
         self.timers.setdefault(name, []).append((a, b))
 
     def routes(self, e, stream):
+        if stream is self.route_stream and self.route_parts > 1:
+            return self.routes_parts(e, stream)
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, dk, k = (c[x] for x in ("B", "C", "H", "half", "dk", "k"))
         self._timed("score_route", stream, lambda: N.call(
@@ -218,6 +232,24 @@ class Pipeline:
             "glsdm_score_route_keys", p(self.qw[e]), p(self.keys), B, C, H, dk, half, k, N.TIE_HIGHEST, 0, C, 1, 0,
             p(self.widx[e]), p(self.ww[e]), p(self.addr[e]), p(self.ckeys[e]), p(self.route_ws),
             self.route_ws.numel(), st))
+
+    def routes_parts(self, e, stream):
+        """The overlap schedule's routes: each route call split over `route_parts`
+        request ranges (same routes bit for bit: requests are independent), and the
+        write route's proposal addresses and keys from one keys launch over the epoch."""
+        N, c, st = self.N, self.cfg, self.N.ctypes.c_void_p(stream.cuda_stream)
+        B, C, H, half, dk, k = (c[x] for x in ("B", "C", "H", "half", "dk", "k"))
+        n = B // self.route_parts
+        at = lambda t, i: N.ctypes.c_void_p(t[i * n:(i + 1) * n].data_ptr())
+        for q, idx, w in ((self.qr[e], self.idx[e], self.w[e]), (self.qw[e], self.widx[e], self.ww[e])):
+            name = "score_route" if q is self.qr[e] else "score_route_keys"
+            for i in range(self.route_parts):
+                self._timed(name, stream, lambda: N.call(
+                    "glsdm_score_route", at(q, i), N.ptr(self.keys), n, C, H, dk, half, k, N.TIE_HIGHEST, None,
+                    at(idx, i), at(w, i), N.ptr(self.route_ws), self.route_ws.numel(), st))
+        self._timed("score_route_keys", stream, lambda: N.call(
+            "glsdm_proposal_keys", N.ptr(self.widx[e]), B, C, H, k, half * half, 0, C, 1, 0, N.ptr(self.addr[e]),
+            N.ptr(self.ckeys[e]), st))
 
     def prepare(self, e, stream):
         """Split commit, first half: group epoch e's entries by address (reads only
@@ -723,6 +755,9 @@ def main():
                     help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
                          "path with the fused proposal commit; proposals-materialised: the same work with "
                          "gathered rows and stored fp32 deltas")
+    ap.add_argument("--route-parts", type=int, default=0,
+                    help="overlap schedule: launch each route call over this many request ranges (0, the "
+                         "default: one part per CU's worth of route blocks for the synthetic-delta path, else 1)")
     ap.add_argument("--split-commit", action="store_true",
                     help="overlap schedule: sort each epoch's write entries on the route stream "
                          "(glsdm_commit_prepare) and apply them on the memory stream (glsdm_commit_apply); "
@@ -743,7 +778,8 @@ def main():
         stack_main(args, dev)
         return
     cfg = CONFIGS[args.config]
-    pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay", args.split_commit)
+    pipe = Pipeline(cfg, dev, args.write_path, args.backward, args.bank == "overlay", args.split_commit,
+                    args.route_parts)
     if args.schedule == "auto":
         args.schedule = "overlap" if pipe.epochs > 1 else "serial"
     unique = pipe.unique_rows()
@@ -866,6 +902,7 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "schedule": args.schedule,
         "split_commit": pipe.split_commit and args.schedule == "overlap",
+        "route_parts": pipe.route_parts if args.schedule == "overlap" else 1,
         "ms_per_step_other_schedule": None if ms_other is None else round(ms_other, 4),
         "higher_is_better": True,
         "scaling": "weak",
