@@ -120,8 +120,10 @@ class Pipeline:
       computes epoch e+1's read and write routes and proposal keys while the
       memory stream runs epoch e's read and commit.  The memory stream waits for
       an epoch's routes with an event; read(e+1) follows commit(e) in stream
-      order, so every read still sees the bank version of its epoch.  Routing is
-      VALU-bound and read/commit HBM-bound, so the two streams share the CUs;
+      order, so every read still sees the bank version of its epoch.  Each route
+      call is launched over `route_parts` request ranges (auto: two at config 2),
+      so at most about one route block per CU runs beside the memory kernels
+      (a full 512-block launch leaves them too few registers; measured);
     * serial: every call on one stream, epoch after epoch (one-epoch steps gain
       nothing from the cross-stream waits).  The per-call durations reported
       next to the step time come from a separate serial pass.
