@@ -120,10 +120,9 @@ class Pipeline:
       computes epoch e+1's read and write routes and proposal keys while the
       memory stream runs epoch e's read and commit.  The memory stream waits for
       an epoch's routes with an event; read(e+1) follows commit(e) in stream
-      order, so every read still sees the bank version of its epoch.  Each route
-      call is launched over `route_parts` request ranges (auto: two at config 2),
-      so at most about one route block per CU runs beside the memory kernels
-      (a full 512-block launch leaves them too few registers; measured);
+      order, so every read still sees the bank version of its epoch.  The write
+      route's proposal keys come from a separate keys launch on the route stream
+      (faster beside the memory kernels than the fused route-with-keys, measured);
     * serial: every call on one stream, epoch after epoch (one-epoch steps gain
       nothing from the cross-stream waits).  The per-call durations reported
       next to the step time come from a separate serial pass.
@@ -194,14 +193,9 @@ class Pipeline:
             self.bw_ws = torch.empty(size.value, dtype=torch.uint8, device=device)
         self.mem_stream = torch.cuda.current_stream(device)
         self.route_stream = torch.cuda.Stream(device)          # default priority
-        # overlap schedule: each route call in `route_parts` launches over consecutive
-        # request ranges, so at most about one fused-route block per CU runs beside the
-        # memory stream's kernels (more leave them too few registers; measured)
-        # (auto: the synthetic-delta write path; the proposal paths' longer memory stream
-        # runs better beside whole launches, measured)
-        tiles = -(-B * C // 64) * H
-        cus = torch.cuda.get_device_properties(device).multi_processor_count
-        parts = route_parts or (max(1, tiles // cus) if write_path == "deltas" else 1)
+        # overlap schedule: each route call launched over `route_parts` consecutive request
+        # ranges (default 1: whole launches)
+        parts = max(1, route_parts)
         while parts > 1 and B % parts:
             parts -= 1
         self.route_parts = parts
@@ -222,7 +216,7 @@ class Pipeline:
         self.timers.setdefault(name, []).append((a, b))
 
     def routes(self, e, stream):
-        if stream is self.route_stream and self.route_parts > 1:
+        if stream is self.route_stream:
             return self.routes_parts(e, stream)
         N, c, p, st = self.N, self.cfg, self.N.ptr, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, dk, k = (c[x] for x in ("B", "C", "H", "half", "dk", "k"))
@@ -236,9 +230,14 @@ class Pipeline:
             self.route_ws.numel(), st))
 
     def routes_parts(self, e, stream):
-        """The overlap schedule's routes: each route call split over `route_parts`
-        request ranges (same routes bit for bit: requests are independent), and the
-        write route's proposal addresses and keys from one keys launch over the epoch."""
+        """The overlap schedule's routes: the read and write routes (each launched over
+        `route_parts` request ranges; the same routes bit for bit, requests are
+        independent), then the write route's proposal addresses and keys from one
+        `glsdm_proposal_keys` launch over the epoch.  Beside the memory stream this
+        runs faster than the write route emitting its keys itself
+        (`glsdm_score_route_keys`, which the serial schedule uses): 0.78 vs 0.92 ms
+        per config-2 step, measured; the memory stream's commit then takes 132 µs
+        instead of 152."""
         N, c, st = self.N, self.cfg, self.N.ctypes.c_void_p(stream.cuda_stream)
         B, C, H, half, dk, k = (c[x] for x in ("B", "C", "H", "half", "dk", "k"))
         n = B // self.route_parts
@@ -757,9 +756,8 @@ def main():
                     help="deltas: synthetic deltas (the BASELINE protocol, default); proposals: the stack's write "
                          "path with the fused proposal commit; proposals-materialised: the same work with "
                          "gathered rows and stored fp32 deltas")
-    ap.add_argument("--route-parts", type=int, default=0,
-                    help="overlap schedule: launch each route call over this many request ranges (0, the "
-                         "default: one part per CU's worth of route blocks for the synthetic-delta path, else 1)")
+    ap.add_argument("--route-parts", type=int, default=1,
+                    help="overlap schedule: launch each route call over this many request ranges")
     ap.add_argument("--split-commit", action="store_true",
                     help="overlap schedule: sort each epoch's write entries on the route stream "
                          "(glsdm_commit_prepare) and apply them on the memory stream (glsdm_commit_apply); "
