@@ -726,7 +726,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, choices=(1, 2, 3, 4, 5), default=2,
                     help="BASELINE.json configs[config-1]; 2 (the headline) is the default; 4 and 5 run the "
                          "layer stack (full forward / decode)")
