@@ -958,18 +958,6 @@ __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t
     for (int64_t i = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * ng + grp; i < count; i += groups) {
         const int64_t hp = aux.long_list[i];
         const int64_t row_addr = (int64_t)(sorted[hp] >> ebits);
-        int len = 1;
-        for (;;) {
-            const int64_t at = hp + len + li;
-            const bool same = at < n && (int64_t)(sorted[at] >> ebits) == row_addr;
-            const uint64_t stop = __ballot(!same) & mine;
-            if (stop == 0) {
-                len += lpr;
-                continue;
-            }
-            len += __ffsll((unsigned long long)(stop >> (grp * lpr))) - 1;
-            break;
-        }
         const TB *row = store.old_row(row_addr);
         float old[CH][VEC], acc[CH][VEC];
 #pragma unroll
@@ -982,53 +970,70 @@ __global__ __launch_bounds__(256) void long_run_kernel(const ROWS store, int64_t
             }
             if (v < nv) VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, old[c]);
         }
-        bool in_order = true;
-        if (keys) {
-            bool ok = true;
-            for (int q = 1 + li; q < len; q += lpr) ok &= key_of(sorted[hp + q]) >= key_of(sorted[hp + q - 1]);
-            in_order = (__ballot(!ok) & mine) == 0;
-        }
-        if (in_order) {
-            // PF entries' delta pieces are fetched before they are added (in order),
-            // so a long run costs one load latency per PF entries, not per entry
-            constexpr int PF = CH * VEC >= 64 ? 1 : (CH * VEC >= 32 ? 2 : 128 / (CH * VEC));
-            for (int q0 = 0; q0 < len; q0 += lpr) {
-                const int q = q0 + li;
-                const int my_ent = q < len ? (int)(sorted[hp + q] & emask) : (int)n;
-                const int cnt = len - q0 < lpr ? len - q0 : lpr;
-                for (int j0 = 0; j0 < cnt; j0 += PF) {
-                    float x[PF][CH][VEC];
-                    bool have[PF];
+        // one pass over the run, lpr positions at a time: each lane fetches one word
+        // (the run's end is the first position of another address), its entry's key
+        // (the run's keys must not fall: checked against the lane before) and, PF
+        // entries at a time, the delta pieces, added in position order.  The sum
+        // assumes arrival order is key order; a run whose keys fall is summed again
+        // below in exact (key, entry) order
+        constexpr int PF = CH * VEC >= 64 ? 1 : (CH * VEC >= 32 ? 2 : 128 / (CH * VEC));
+        int len = 0;
+        bool ok = true;
+        int64_t carry = INT64_MIN;                      // the key before this chunk's first position
+        for (;;) {
+            const int64_t at = hp + len + li;
+            const uint64_t w = at < n ? sorted[at] : ~0ull;
+            const bool same = at < n && (int64_t)(w >> ebits) == row_addr;
+            const uint64_t stop = __ballot(!same) & mine;
+            const int cnt = stop ? __ffsll((unsigned long long)(stop >> (grp * lpr))) - 1 : lpr;
+            const int my_ent = li < cnt ? (int)(w & emask) : (int)n;
+            if (keys) {
+                const int64_t k = li < cnt ? key_of(w) : INT64_MAX;
+                int64_t before = __shfl_up(k, 1, lpr);
+                if (li == 0) before = carry;
+                ok &= li >= cnt || k >= before;
+                carry = __shfl(k, grp * lpr + (cnt > 0 ? cnt - 1 : 0));
+            }
+            for (int j0 = 0; j0 < cnt; j0 += PF) {
+                float x[PF][CH][VEC];
+                bool have[PF];
 #pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        const int j = j0 + u;
-                        const int ent = __shfl(my_ent, grp * lpr + (j < cnt ? j : 0));
-                        have[u] = j < cnt && ent < n;
-                        if (have[u]) {
-                            const typename SRC::Entry e = src.entry(ent);
+                for (int u = 0; u < PF; ++u) {
+                    const int j = j0 + u;
+                    const int ent = __shfl(my_ent, grp * lpr + (j < cnt ? j : 0));
+                    have[u] = j < cnt && ent < n;
+                    if (have[u]) {
+                        const typename SRC::Entry e = src.entry(ent);
 #pragma unroll
-                            for (int c = 0; c < CH; ++c) {
-                                const int v = li + c * lpr;
-                                if (v < nv) src.template get<VEC>(e, v, old[c], x[u][c]);
-                            }
+                        for (int c = 0; c < CH; ++c) {
+                            const int v = li + c * lpr;
+                            if (v < nv) src.template get<VEC>(e, v, old[c], x[u][c]);
                         }
                     }
+                }
 #pragma unroll
-                    for (int u = 0; u < PF; ++u) {
-                        if (have[u]) {
+                for (int u = 0; u < PF; ++u) {
+                    if (have[u]) {
 #pragma unroll
-                            for (int c = 0; c < CH; ++c) {
-                                const int v = li + c * lpr;
-                                if (v < nv) {
+                        for (int c = 0; c < CH; ++c) {
+                            const int v = li + c * lpr;
+                            if (v < nv) {
 #pragma unroll
-                                    for (int y = 0; y < VEC; ++y) acc[c][y] += x[u][c][y];
-                                }
+                                for (int y = 0; y < VEC; ++y) acc[c][y] += x[u][c][y];
                             }
                         }
                     }
                 }
             }
-        } else {
+            len += cnt;
+            if (stop) break;
+        }
+        const bool in_order = (__ballot(!ok) & mine) == 0;
+        if (!in_order) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int x = 0; x < VEC; ++x) acc[c][x] = 0.0f;   // the run again, in (key, entry) order
             int64_t last_k = INT64_MIN, last_e = -1;
             for (int r2 = 0; r2 < len; ++r2) {
                 int64_t best_k = INT64_MAX, best_e = INT64_MAX;
