@@ -42,6 +42,8 @@
 #include <atomic>
 #include <mutex>
 
+#include <type_traits>
+
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -664,7 +666,17 @@ template <typename TD> struct StoredDeltas {
     template <int VEC>
     __device__ __forceinline__ void get(const Entry &e, int v, const float (&)[VEC], float (&x)[VEC]) const
     {
-        VecLoad<TD, VEC>::load(e.src + (int64_t)v * VEC, x);
+        if constexpr (VEC * sizeof(TD) == 16 && std::is_same<TD, bf16_t>::value) {
+            const uint4 u = load16_stream(e.src + (int64_t)v * VEC);   // each delta is read once
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[2 * i] = __uint_as_float(w[i] << 16);
+                x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+            }
+        } else {
+            VecLoad<TD, VEC>::load(e.src + (int64_t)v * VEC, x);
+        }
     }
 };
 
@@ -911,7 +923,15 @@ __global__ __launch_bounds__(256) void segment_kernel(const ROWS store, int64_t 
             if (v < nv) {
 #pragma unroll
                 for (int x = 0; x < VEC; ++x) old[c][x] = old[c][x] + acc[c][x];
-                VecStore<TB, VEC>::store(dst + (int64_t)v * VEC, old[c]);
+                if constexpr (VEC * sizeof(TB) == 16 && std::is_same<TB, bf16_t>::value) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        w[i] = (uint32_t)f32_to_bf16(old[c][2 * i]) | ((uint32_t)f32_to_bf16(old[c][2 * i + 1]) << 16);
+                    store16_stream(dst + (int64_t)v * VEC, make_uint4(w[0], w[1], w[2], w[3]));
+                } else {
+                    VecStore<TB, VEC>::store(dst + (int64_t)v * VEC, old[c]);
+                }
             }
         }
     }

@@ -214,6 +214,32 @@ template <int VEC> struct VecLoad<bf16_t, VEC> {
     }
 };
 
+#ifndef GLSDM_NT
+#define GLSDM_NT 1
+#endif
+typedef unsigned int glsdm_u32x4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte load / store with the nontemporal hint (data used once: streamed
+// past the caches' replacement), when GLSDM_NT is set.
+__device__ __forceinline__ uint4 load16_stream(const void *p)
+{
+#if GLSDM_NT
+    const glsdm_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const glsdm_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4 *>(p);
+#endif
+}
+__device__ __forceinline__ void store16_stream(void *p, uint4 u)
+{
+#if GLSDM_NT
+    glsdm_u32x4 v = {u.x, u.y, u.z, u.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<glsdm_u32x4 *>(p));
+#else
+    *reinterpret_cast<uint4 *>(p) = u;
+#endif
+}
+
 template <typename T, int VEC> struct VecStore;
 
 template <int VEC> struct VecStore<float, VEC> {

@@ -9,6 +9,8 @@
 // flight at once; partial sums are combined across those lane groups with
 // __shfl_xor and the first group stores the row.  Products are rounded before
 // the add (no FMA contraction), as in the reference's rows * w then sum.
+#include <type_traits>
+
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -50,7 +52,17 @@ __global__ __launch_bounds__(256) void read_kernel(const TB *__restrict__ bank, 
             const int v = li + c * lpr;
             if (v < nv) {
                 float x[VEC];
-                VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, x);
+                if constexpr (VEC * sizeof(TB) == 16 && std::is_same<TB, bf16_t>::value) {
+                    const uint4 u = load16_stream(row + (int64_t)v * VEC);    // random rows: little reuse
+                    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[2 * i] = __uint_as_float(wd[i] << 16);
+                        x[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+                    }
+                } else {
+                    VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, x);
+                }
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) acc[c][e] += x[e] * w;
             }
