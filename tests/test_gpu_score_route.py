@@ -119,6 +119,8 @@ def _check_filtered(device, q, k, width, tie):
     (8, 512, 8, 128, 256, 16),     # config 2's epoch
     (1, 77, 3, 64, 64, 9),         # one chunk per factor, ragged tokens
     (2, 45, 2, 256, 128, 12),
+    (2, 33, 1, 64, 128, 16),       # two chunks per factor, scores held in registers
+    (1, 100, 2, 128, 192, 16),     # three chunks per factor, scores held in registers
     (1, 130, 1, 128, 320, 16),     # five chunks: a partial group of maxima
     (1, 64, 2, 64, 512, 15),
 ])
