@@ -52,10 +52,10 @@ CFG = CONFIGS[2]
 # WRITE x 1.0); source: profiles/glsdm_kernels.config2.hbm-traffic.md.  Re-measured
 # whenever a kernel of the path changes.
 TRAFFIC_PER_LAUNCH = {
-    "score_route": (4852.8 * 1.9998 + 10240.0) * 1024,
-    "read": (67334.2 * 1.9998 + 16384.0) * 1024,
+    "score_route": (4911.6 * 1.9998 + 7782.4) * 1024,
+    "read": (67885.0 * 1.9998 + 16384.0) * 1024,
     # glsdm_commit on the bucket path: tile bucketing, bucket sort, segment
-    "commit": ((2094.6 + 2612.3 + 133290.2) * 1.9998 + (6144.1 + 4100.5 + 120860.8)) * 1024,
+    "commit": ((2094.6 + 2601.8 + 132820.3) * 1.9998 + (6144.1 + 4100.5 + 120860.8)) * 1024,
 }
 
 
