@@ -15,7 +15,7 @@
 
 namespace glsdm {
 
-template <typename TB, typename TO, int VEC, int CH>
+template <typename TB, typename TO, int VEC, int CH, int U>
 __global__ __launch_bounds__(256) void read_kernel(const TB *__restrict__ bank, int64_t H, int64_t S,
                                                    int64_t D, int64_t T, int width,
                                                    const int64_t *__restrict__ index,
@@ -41,30 +41,62 @@ __global__ __launch_bounds__(256) void read_kernel(const TB *__restrict__ bank, 
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[c][e] = 0.0f;
 
-#pragma unroll 4
-    for (int j = grp; j < width; j += ng) {
-        const int64_t slot = ix[j];
-        const float w = wt[j];
-        if (slot < 0 || slot >= S) continue;
-        const TB *row = base + slot * D;
+    // U route entries per lane group at a time: their slots and weights are loaded
+    // first, then all U row loads are issued before any is used (an out-of-range
+    // slot reads row 0 and adds nothing), so a wave keeps U rows per group in flight
+    // instead of waiting on each slot before its row.  The entries are still added in
+    // the order j = grp, grp + ng, ...: the same bits for every U.
+    for (int j0 = grp; j0 < width; j0 += U * ng) {
+        int64_t slot[U];
+        float w[U];
+        bool ok[U];
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int v = li + c * lpr;
-            if (v < nv) {
-                float x[VEC];
-                if constexpr (VEC * sizeof(TB) == 16 && std::is_same<TB, bf16_t>::value) {
-                    const uint4 u = load16_stream(row + (int64_t)v * VEC);    // random rows: little reuse
-                    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * ng;
+            const bool in = j < width;
+            const int jj = in ? j : width - 1;             // a valid position: loads stay unconditional
+            slot[u] = ix[jj];
+            w[u] = wt[jj];
+            ok[u] = in && slot[u] >= 0 && slot[u] < S;
+        }
+        // lanes past the row's last piece load its last piece again (unconditional
+        // loads, no branch between them) and never store what they sum
+        constexpr bool RAW = VEC * sizeof(TB) == 16 && std::is_same<TB, bf16_t>::value;
+        uint4 raw[U][CH];
+        float x[RAW ? 1 : U][CH][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const TB *row = base + (ok[u] ? slot[u] : 0) * D;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int v = li + c * lpr < nv ? li + c * lpr : nv - 1;
+                if constexpr (RAW)
+                    raw[u][c] = load16_stream(row + (int64_t)v * VEC);    // random rows: little reuse
+                else
+                    VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, x[u][c]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                float y[VEC];
+                if constexpr (RAW) {
+                    const uint32_t wd[4] = {raw[u][c].x, raw[u][c].y, raw[u][c].z, raw[u][c].w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        x[2 * i] = __uint_as_float(wd[i] << 16);
-                        x[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+                        y[2 * i] = __uint_as_float(wd[i] << 16);
+                        y[2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
                     }
                 } else {
-                    VecLoad<TB, VEC>::load(row + (int64_t)v * VEC, x);
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) y[e] = x[u][c][e];
                 }
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) acc[c][e] += x[e] * w;
+                for (int e = 0; e < VEC; ++e) {
+                    const float sum = acc[c][e] + y[e] * w[u];
+                    acc[c][e] = ok[u] ? sum : acc[c][e];
+                }
             }
         }
     }
@@ -83,20 +115,37 @@ __global__ __launch_bounds__(256) void read_kernel(const TB *__restrict__ bank, 
     }
 }
 
+template <typename TB, typename TO, int VEC, int CH>
+static void launch_read_u(const TB *bk, int64_t H, int64_t S, int64_t D, int64_t T, int width,
+                          const int64_t *index, const float *weights, TO *o, int64_t rows, const RowPlan &p,
+                          bool narrow, hipStream_t st)
+{
+    // wide: several route entries per lane group in flight; narrow: one (at most 32
+    // VGPRs for 16-byte pieces, so eight of its waves leave a SIMD room for one wave of
+    // the 248-VGPR route kernel when both run at once)
+    constexpr int U = CH <= 2 ? 4 : (CH <= 4 ? 2 : 1);
+    const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
+    if (narrow || U == 1)
+        hipLaunchKernelGGL((read_kernel<TB, TO, VEC, CH, 1>), grid, block, 0, st, bk, H, S, D, T, width, index,
+                           weights, o, rows, p.nv, p.lpr);
+    else
+        hipLaunchKernelGGL((read_kernel<TB, TO, VEC, CH, U>), grid, block, 0, st, bk, H, S, D, T, width, index,
+                           weights, o, rows, p.nv, p.lpr);
+}
+
 template <typename TB, typename TO, int VEC>
 static int launch_read_ch(const void *bank, int64_t H, int64_t S, int64_t D, int64_t T, int width,
                           const int64_t *index, const float *weights, void *out, int64_t rows,
-                          const RowPlan &p, hipStream_t st)
+                          const RowPlan &p, bool narrow, hipStream_t st)
 {
-    const dim3 grid((unsigned)ceil_div(rows, 4)), block(256);
     const TB *bk = static_cast<const TB *>(bank);
     TO *o = static_cast<TO *>(out);
     switch (p.ch) {
-    case 1: hipLaunchKernelGGL((read_kernel<TB, TO, VEC, 1>), grid, block, 0, st, bk, H, S, D, T, width, index, weights, o, rows, p.nv, p.lpr); break;
-    case 2: hipLaunchKernelGGL((read_kernel<TB, TO, VEC, 2>), grid, block, 0, st, bk, H, S, D, T, width, index, weights, o, rows, p.nv, p.lpr); break;
+    case 1: launch_read_u<TB, TO, VEC, 1>(bk, H, S, D, T, width, index, weights, o, rows, p, narrow, st); break;
+    case 2: launch_read_u<TB, TO, VEC, 2>(bk, H, S, D, T, width, index, weights, o, rows, p, narrow, st); break;
     case 3:
-    case 4: hipLaunchKernelGGL((read_kernel<TB, TO, VEC, 4>), grid, block, 0, st, bk, H, S, D, T, width, index, weights, o, rows, p.nv, p.lpr); break;
-    default: hipLaunchKernelGGL((read_kernel<TB, TO, VEC, 8>), grid, block, 0, st, bk, H, S, D, T, width, index, weights, o, rows, p.nv, p.lpr); break;
+    case 4: launch_read_u<TB, TO, VEC, 4>(bk, H, S, D, T, width, index, weights, o, rows, p, narrow, st); break;
+    default: launch_read_u<TB, TO, VEC, 8>(bk, H, S, D, T, width, index, weights, o, rows, p, narrow, st); break;
     }
     return check_launch("read_kernel");
 }
@@ -104,21 +153,21 @@ static int launch_read_ch(const void *bank, int64_t H, int64_t S, int64_t D, int
 template <typename TB, typename TO>
 static int launch_read_t(const void *bank, int64_t H, int64_t S, int64_t D, int64_t T, int width,
                          const int64_t *index, const float *weights, void *out, int64_t rows,
-                         hipStream_t st)
+                         bool narrow, hipStream_t st)
 {
     constexpr int FULL = 16 / sizeof(TB);
     RowPlan p = row_plan(D, sizeof(TB));
     // 16-byte accesses need 16-byte aligned base pointers (D % FULL == 0 keeps rows aligned).
     const bool aligned = ((reinterpret_cast<uintptr_t>(bank) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
     if (p.vec == FULL && aligned)
-        return launch_read_ch<TB, TO, FULL>(bank, H, S, D, T, width, index, weights, out, rows, p, st);
+        return launch_read_ch<TB, TO, FULL>(bank, H, S, D, T, width, index, weights, out, rows, p, narrow, st);
     p = RowPlan{1, (int)D, D < 64 ? pow2_ceil(D) : 64, (int)ceil_div(D, 64)};
-    return launch_read_ch<TB, TO, 1>(bank, H, S, D, T, width, index, weights, out, rows, p, st);
+    return launch_read_ch<TB, TO, 1>(bank, H, S, D, T, width, index, weights, out, rows, p, narrow, st);
 }
 
 int read_launch(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                 int64_t T, int32_t width, const int64_t *index, const float *weights, void *out,
-                int32_t out_dtype, hipStream_t st)
+                int32_t out_dtype, hipStream_t st, bool narrow)
 {
     if (B < 0 || H < 1 || S < 1 || D < 1 || T < 0 || width < 1)
         return fail(GLSDM_ERR_ARG, "read: bad shape B=%lld H=%lld S=%lld D=%lld T=%lld width=%d",
@@ -131,12 +180,12 @@ int read_launch(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int6
     if (D > max_d) return fail(GLSDM_ERR_UNSUPPORTED, "read: D=%lld above %lld", (long long)D, (long long)max_d);
     if (!bank || !index || !weights || !out) return fail(GLSDM_ERR_ARG, "read: null pointer");
     if (bank_dtype == GLSDM_F32 && out_dtype == GLSDM_F32)
-        return launch_read_t<float, float>(bank, H, S, D, T, width, index, weights, out, rows, st);
+        return launch_read_t<float, float>(bank, H, S, D, T, width, index, weights, out, rows, narrow, st);
     if (bank_dtype == GLSDM_BF16 && out_dtype == GLSDM_F32)
-        return launch_read_t<bf16_t, float>(bank, H, S, D, T, width, index, weights, out, rows, st);
+        return launch_read_t<bf16_t, float>(bank, H, S, D, T, width, index, weights, out, rows, narrow, st);
     if (bank_dtype == GLSDM_F32 && out_dtype == GLSDM_BF16)
-        return launch_read_t<float, bf16_t>(bank, H, S, D, T, width, index, weights, out, rows, st);
-    return launch_read_t<bf16_t, bf16_t>(bank, H, S, D, T, width, index, weights, out, rows, st);
+        return launch_read_t<float, bf16_t>(bank, H, S, D, T, width, index, weights, out, rows, narrow, st);
+    return launch_read_t<bf16_t, bf16_t>(bank, H, S, D, T, width, index, weights, out, rows, narrow, st);
 }
 
 // ------------------------------------------------------------ gather / addresses
@@ -176,7 +225,15 @@ extern "C" int glsdm_read(const void *bank, int32_t bank_dtype, int64_t B, int64
                           const float *weights, void *out, int32_t out_dtype, void *stream)
 {
     return read_launch(bank, bank_dtype, B, H, S, D, T, width, index, weights, out, out_dtype,
-                       as_stream(stream));
+                       as_stream(stream), false);
+}
+
+extern "C" int glsdm_read_narrow(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S,
+                                 int64_t D, int64_t T, int32_t width, const int64_t *index,
+                                 const float *weights, void *out, int32_t out_dtype, void *stream)
+{
+    return read_launch(bank, bank_dtype, B, H, S, D, T, width, index, weights, out, out_dtype,
+                       as_stream(stream), true);
 }
 
 namespace glsdm {
@@ -197,7 +254,7 @@ extern "C" int glsdm_route_read(const void *bank, int32_t bank_dtype, int64_t B,
     int rc = glsdm::route_launch(scores, scores_dtype, B * T * H, (int)half, width, tie, workspace,
                                  workspace_bytes, index, weights, st);
     if (rc != GLSDM_OK) return rc;
-    return read_launch(bank, bank_dtype, B, H, S, D, T, width, index, weights, out, out_dtype, st);
+    return read_launch(bank, bank_dtype, B, H, S, D, T, width, index, weights, out, out_dtype, st, false);
 }
 
 extern "C" int glsdm_gather_rows(const void *bank, int32_t bank_dtype, int64_t rows, int64_t D,

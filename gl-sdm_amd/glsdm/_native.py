@@ -27,6 +27,7 @@ SIGNATURES = {
     "glsdm_route": ([_P, _I32, _I64, _I32, _I32, _I32, _P, _P, _P, _SZ, _P], _I32),
     "glsdm_route_workspace_bytes": ([_I64, _I32, _I32, _P], _I32),
     "glsdm_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _I32, _P], _I32),
+    "glsdm_read_narrow": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _I32, _P], _I32),
     "glsdm_route_read": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _I32, _P, _I32, _P, _P, _P, _SZ,
                           _P], _I32),
     "glsdm_score": ([_P, _P, _I64, _I64, _I64, _I32, _I32, _P, _P], _I32),

@@ -141,7 +141,8 @@ def route(scores, count, tie="lowest"):
     return _route(_route_scores(scores), count, tie)
 
 
-def _read(values, index, weights, out_dtype):
+def _read(values, index, weights, out_dtype, narrow=False):
+    """``narrow``: ``glsdm_read_narrow`` (the same bits; fits beside the route kernel)."""
     device = require_cuda(values, index, weights)
     B, H, S, D = values.shape
     if index.ndim != 4 or index.shape[0] != B or index.shape[2] != H or weights.shape != index.shape:
@@ -151,8 +152,8 @@ def _read(values, index, weights, out_dtype):
     T, width = index.shape[1], index.shape[3]
     N.check_range(index, S, "snapshot_read")
     out = torch.empty((B, T, H, D), dtype=out_dtype, device=device)
-    N.call("glsdm_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T, width, N.ptr(index),
-           N.ptr(weights), N.ptr(out), N.dtype_code(out), N.stream(device))
+    N.call("glsdm_read_narrow" if narrow else "glsdm_read", N.ptr(values), N.dtype_code(values), B, H, S, D, T,
+           width, N.ptr(index), N.ptr(weights), N.ptr(out), N.dtype_code(out), N.stream(device))
     return out
 
 

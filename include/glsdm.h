@@ -96,6 +96,18 @@ int glsdm_read(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64
                void *out, int32_t out_dtype, void *stream);
 
 /*
+ * glsdm_read with one route entry per lane group in flight (glsdm_read keeps up to
+ * four): the same arguments and the same bits, slower alone (config 2: 38 vs 32 us)
+ * but small enough (at most 32 VGPRs for 16-byte row pieces) that its waves leave
+ * each SIMD room for a wave of the fused route kernel, for a read that runs while
+ * another stream routes.  No counterpart in the reference (its read is one torch
+ * gather); for callers that overlap reading with routing on two streams.
+ */
+int glsdm_read_narrow(const void *bank, int32_t bank_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                      int64_t T, int32_t width, const int64_t *index, const float *weights,
+                      void *out, int32_t out_dtype, void *stream);
+
+/*
  * Route then read (glsdm_route followed by glsdm_read on the same stream).
  *   scores [B, T, H, 2*half] of scores_dtype (fp32 or bf16) with half*half == S;
  *   workspace as glsdm_route, for rows = B*T*H.

@@ -10,7 +10,7 @@ from _util import header_functions
 
 def test_header_declares_the_expected_surface():
     names = header_functions()
-    for required in ("glsdm_route", "glsdm_read", "glsdm_route_read", "glsdm_score", "glsdm_commit",
+    for required in ("glsdm_route", "glsdm_read", "glsdm_read_narrow", "glsdm_route_read", "glsdm_score", "glsdm_commit",
                      "glsdm_commit_workspace_bytes", "glsdm_absolute_addresses", "glsdm_proposal_keys",
                      "glsdm_gather_rows", "glsdm_version", "glsdm_last_error", "glsdm_proposal_error",
                      "glsdm_proposal_delta", "glsdm_commit_proposals", "glsdm_route_backward",

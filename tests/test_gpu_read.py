@@ -35,6 +35,28 @@ def test_read_matches_oracle(device, dtype, B, H, S, D, T, k):
     torch.testing.assert_close(out.cpu(), torch_oracle.read(mem.float(), idx, w), atol=1e-6, rtol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,S,D,T,k", [
+    (2, 8, 256, 128, 33, 16),      # config 2 geometry: four entries per lane group in flight
+    (1, 1, 1024, 512, 20, 32),     # config 3 geometry: one lane group per wave
+    (2, 2, 16, 8, 17, 3),          # ragged: the last batch of entries is partial
+    (1, 1, 16, 2048, 3, 5),        # two pieces per lane: two entries in flight
+    (3, 2, 67, 37, 4, 3),          # scalar pieces
+])
+def test_read_narrow_equals_wide(device, dtype, B, H, S, D, T, k):
+    """glsdm_read (several entries per lane group in flight) and glsdm_read_narrow
+    (one) add the same products in the same order: bitwise equal, and the oracle's."""
+    mem, idx, w = _case(B, H, S, D, T, k, dtype, seed=7 * S + D + k)
+    idx[0, 0, 0, k - 1] = S                       # an out-of-range slot adds nothing in both
+    args = (mem.to(device), idx.to(device), w.to(device), torch.float32)
+    wide, narrow = hip._read(*args), hip._read(*args, narrow=True)
+    keep = (idx >= 0) & (idx < S)
+    ref = c_oracle.read(mem, idx.clamp(0, S - 1), w * keep)
+    torch.testing.assert_close(wide.cpu(), ref, atol=1e-6, rtol=1e-5)
+    torch.testing.assert_close(narrow.cpu(), ref, atol=1e-6, rtol=1e-5)
+    assert torch.equal(wide, narrow)
+
+
 def test_read_bf16_output(device):
     mem, idx, w = _case(2, 8, 256, 128, 16, 16, torch.bfloat16, seed=1)
     out = hip.snapshot_read(mem.to(device), idx.to(device), w.to(device), out_dtype=torch.bfloat16)
