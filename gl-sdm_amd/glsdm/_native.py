@@ -47,6 +47,7 @@ SIGNATURES = {
     "glsdm_qk_norm_rotary": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
     "glsdm_gate_merge": ([_P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "glsdm_relu2_gate": ([_P, _I32, _I64, _I64, _P, _P], _I32),
+    "glsdm_linear_small": ([_P, _P, _P, _P, _I64, _I64, _I64, _P], _I32),
     "glsdm_rms_norm_cast": ([_P, _I32, _P, _I32, _I64, _I64, ctypes.c_float, _P, _I32, _P], _I32),
     "glsdm_write_gates": ([_P, _P, _I32, _I64, _P, _P, _P], _I32),
     "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),
@@ -149,7 +150,11 @@ def ptr(t):
 
 
 def stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The current HIP stream of ``device`` as a ctypes pointer (torch's raw-stream
+    query: a decode step makes over a hundred native calls, and the Stream-object
+    path costs several microseconds of host time each)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
 
 
 def dtype_code(t):

@@ -21,6 +21,7 @@ from torch import nn
 import torch.nn.functional as F
 
 from .. import _native as N
+from .common import linear
 
 
 def qk_norm_rotary(x, freq, offset):
@@ -157,9 +158,9 @@ class Transformer(nn.Module):
     def forward(self, x, cache=None):
         B, T, D = x.shape
         dk = self.head_dim
-        q, gate = self.q(x).view(B, T, self.num_heads, 2 * dk).chunk(2, -1)
-        k = self.k(x).view(B, T, self.num_kv_heads, dk)
-        v = self.v(x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
+        q, gate = linear(self.q, x).view(B, T, self.num_heads, 2 * dk).chunk(2, -1)
+        k = linear(self.k, x).view(B, T, self.num_kv_heads, dk)
+        v = linear(self.v, x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
         previous = cache["k"].shape[2] if cache and cache.get("k") is not None else 0
         offset = 0 if cache is None else cache.get("tokens", previous)
         fused = (x.is_cuda and dk in (4, 8, 16, 32, 64, 128, 256) and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
@@ -197,5 +198,5 @@ class Transformer(nn.Module):
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
         if fused and out.stride(-1) == 1 and gate.stride(-1) == 1 and not (
                 torch.is_grad_enabled() and (out.requires_grad or gate.requires_grad)):
-            return self.proj(gate_merge(out, gate))
-        return self.proj(out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid())
+            return linear(self.proj, gate_merge(out, gate))
+        return linear(self.proj, out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid())

@@ -1,12 +1,33 @@
 """RMSNorm and the gated squared-ReLU MLP of S/layers/common.py:7-27
 (S/ = projects/gl-sdm/src/gl_sdm/).  On the GPU outside autograd the MLP's
 activation ``gate * relu(u)^2`` is one HIP launch (``glsdm_relu2_gate``, the
-same roundings as the tensor ops)."""
+same roundings as the tensor ops), and the stack's projections of decode-sized
+inputs run ``glsdm_linear_small`` (``linear``)."""
 import torch
 from torch import nn
 import torch.nn.functional as F
 
 from .. import _native as N
+
+
+def linear(layer, x):
+    """``layer(x)`` for an ``nn.Linear``.  Outside autograd, a bf16 input of at most
+    64 rows on the device with a bf16 weight (out features a multiple of 16, in
+    features of 128) runs ``glsdm_linear_small``: fp32 accumulation rounded once,
+    as torch's bf16 linear, in the kernel's own summation order (results agree to
+    the rounding of the fp32 sum).  A decode step makes over a hundred of these
+    calls; the library GEMM's host cost per call (~20 us) is what bounds that step."""
+    w = layer.weight
+    K = x.shape[-1]
+    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and x.numel() <= 64 * K and w.shape[0] % 16 == 0 and K % 128 == 0 and x.is_contiguous()
+            and x.data_ptr() % 16 == 0 and w.is_contiguous()
+            and (layer.bias is None or layer.bias.dtype == torch.bfloat16)):
+        out = torch.empty((*x.shape[:-1], w.shape[0]), dtype=torch.bfloat16, device=x.device)
+        N.call("glsdm_linear_small", N.ptr(x), N.ptr(w), N.ptr(layer.bias), N.ptr(out), x.numel() // K, w.shape[0],
+               K, N.stream(x.device))
+        return out
+    return layer(x)
 
 
 def relu2_gate(h):
@@ -55,11 +76,11 @@ class MLP(nn.Module):
         self.proj = nn.Linear(inner, dim)
 
     def forward(self, x):
-        h = self.fc(x)
+        h = linear(self.fc, x)
         inner = h.shape[-1] // 2
         if (h.is_cuda and h.dtype in (torch.float32, torch.bfloat16) and h.is_contiguous()
                 and inner % (16 // h.element_size()) == 0 and h.data_ptr() % 16 == 0
                 and not (torch.is_grad_enabled() and h.requires_grad)):
-            return self.proj(relu2_gate(h))
+            return linear(self.proj, relu2_gate(h))
         u, gate = h.chunk(2, -1)
-        return self.proj(gate * u.relu().square())
+        return linear(self.proj, gate * u.relu().square())

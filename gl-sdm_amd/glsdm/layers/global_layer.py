@@ -9,7 +9,7 @@ from .. import _native as N
 from ..memory import routing
 from ..memory.proposals import layer_proposal, log_proposal
 from .block import check_reg_mode, regulariser, zero
-from .common import MLP, RMSNorm
+from .common import MLP, RMSNorm, linear
 from .router import GlobalRouter
 
 
@@ -42,9 +42,9 @@ class GlobalLayer(nn.Module):
         B, T, _ = x.shape
         router = self.attn
         dtype = router.q.weight.dtype
-        scores = router.q(self.norm1.cast(x, dtype)).view(B, T, router.heads, -1)
+        scores = linear(router.q, self.norm1.cast(x, dtype)).view(B, T, router.heads, -1)
         readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
-        x = x + router.proj(router.read_norm(readings.to(dtype)).flatten(-2))
+        x = x + linear(router.proj, router.read_norm(readings.to(dtype)).flatten(-2))
         x = x + self.mlp(self.norm2.cast(x, dtype))
         return x, regulariser(x, self.reg_mode), zero(x)
 
@@ -66,12 +66,12 @@ class GlobalLayer(nn.Module):
         B, T, _ = x.shape
         router = self.attn
         zk = self.norm1.cast(x, router.k.weight.dtype)
-        scores = router.k(zk).view(B, T, router.heads, -1)
+        scores = linear(router.k, zk).view(B, T, router.heads, -1)
         prediction, index, weights = routing.routed_read(self, snapshot.values, scores, router.num_writes, physical)
         vdt = router.v.weight.dtype
         dense = zk if vdt == zk.dtype else self.norm1.cast(x, vdt)
-        target = router.v(dense).view(B, T, router.heads, router.head_dim)
-        b_lin, d_lin = router.beta(dense), router.decay(dense)
+        target = linear(router.v, dense).view(B, T, router.heads, router.head_dim)
+        b_lin, d_lin = linear(router.beta, dense), linear(router.decay, dense)
         if log is not None and not training and b_lin.is_cuda and b_lin.dtype in (torch.float32, torch.bfloat16):
             return log_proposal(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx,
                                 chunk_size, num_layers)

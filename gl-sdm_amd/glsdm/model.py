@@ -10,7 +10,7 @@ import torch
 from torch import nn
 import torch.nn.functional as F
 
-from .layers.common import RMSNorm
+from .layers.common import RMSNorm, linear
 from .layers.stack import forward as stack_forward, make_layers
 from .memory import MemoryBank
 
@@ -39,7 +39,7 @@ class Model(nn.Module):
         self.to(dtype=getattr(torch, cfg.get("dtype", "bfloat16")))
 
     def head(self, x):
-        return soft_cap(self.proj(self.norm(x).to(self.proj.weight.dtype)).float())
+        return soft_cap(linear(self.proj, self.norm(x).to(self.proj.weight.dtype)).float())
 
     def hidden(self, inputs, cache=None):
         x = self.embed(inputs)

@@ -496,6 +496,21 @@ int glsdm_gate_merge(const void *o, const int64_t *o_strides, const void *gate, 
 int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner, void *out, void *stream);
 
 /*
+ * A bf16 projection of at most 64 rows (decode):
+ *   out [M, N] = bf16(sum_k x[m, k] * weight[n, k] + bias[n]), fp32 accumulation
+ *   rounded once (round-to-nearest-even); bias may be NULL.
+ * M <= 64, N a multiple of 16, K a multiple of 128; x and weight 16-byte aligned
+ * (GLSDM_ERR_UNSUPPORTED otherwise, nothing launched).  The fp32 summation order
+ * is the kernel's own: results agree with torch's bf16 linear to the rounding of
+ * the fp32 sum.
+ * Replaces: the nn.Linear projections of S/layers/attention.py:11-42,
+ * S/layers/common.py:21-27, S/layers/router.py:13-36 and the head of
+ * S/model.py:84-96 for decode-sized inputs (torch.nn.functional.linear).
+ */
+int glsdm_linear_small(const void *x, const void *weight, const void *bias, void *out, int64_t M, int64_t N,
+                       int64_t K, void *stream);
+
+/*
  * RMSNorm then a cast: per row of x [rows, dim] (x_dtype), r =
  * rsqrt(mean(x^2) + eps), y = (x*r)*w in fp32 rounded to x_dtype (w [dim] of
  * w_dtype, rounded to x_dtype first), y written as out_dtype to out [rows, dim].

@@ -137,3 +137,47 @@ def test_write_gates_match_tensor_ops(device, dtype):
     assert beta.shape == ref_beta.shape == log_decay.shape
     torch.testing.assert_close(beta, ref_beta, atol=1e-7, rtol=4e-7)
     torch.testing.assert_close(log_decay, ref_ld, atol=1e-7, rtol=4e-7)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [
+    (64, 3072, 1024, True),        # the config-5 decode projections: 64 streams x one token
+    (64, 16, 1024, True),          # a write-gate projection (one column tile)
+    (17, 1024, 4096, True),        # ragged rows, a long reduction (the MLP's down projection)
+    (1, 32000, 1024, False),       # one row through the vocabulary head (no bias)
+    (40, 48, 128, True),           # the smallest reduction
+])
+def test_linear_small_matches_float64_and_torch(device, M, N, K, bias):
+    """glsdm_linear_small: fp32 accumulation rounded once to bf16, so within a bf16
+    rounding of the float64 result and of torch's bf16 linear (the fp32 summation
+    orders differ); a dropped bias, a transposed weight or a lost reduction quarter
+    would be far outside that."""
+    from glsdm.layers.common import linear
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    lin = torch.nn.Linear(K, N, bias=bias).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(N, K, generator=g) / K ** 0.5).to(device))
+        if bias:
+            lin.bias.copy_((torch.randn(N, generator=g) * 0.5).to(device))
+    x = torch.randn(M, K, generator=g).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        out = linear(lin, x)
+        ref_torch = torch.nn.functional.linear(x, lin.weight, lin.bias)
+    ref = x.double().cpu() @ lin.weight.double().cpu().T
+    if bias:
+        ref = ref + lin.bias.double().cpu()
+    assert out.dtype == torch.bfloat16 and out.shape == (M, N)
+    scale = ref.abs().max().item()
+    torch.testing.assert_close(out.double().cpu(), ref, rtol=8e-3, atol=1e-3 * scale)
+    torch.testing.assert_close(out.float(), ref_torch.float(), rtol=8e-3, atol=1e-3 * scale)
+    # most elements round to the same bf16 as torch's
+    assert (out == ref_torch).float().mean().item() > 0.9
+
+
+def test_linear_small_falls_back_for_other_shapes(device):
+    """Inputs the kernel does not take (more than 64 rows, K not a multiple of 128,
+    fp32, under autograd) go through torch's linear unchanged."""
+    from glsdm.layers.common import linear
+    lin = torch.nn.Linear(96, 32).to(device=device, dtype=torch.bfloat16)
+    x = torch.randn(65, 96, device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        assert torch.equal(linear(lin, x), lin(x))
