@@ -151,7 +151,7 @@ def test_linear_small_matches_float64_and_torch(device, M, N, K, bias):
     rounding of the float64 result and of torch's bf16 linear (the fp32 summation
     orders differ); a dropped bias, a transposed weight or a lost reduction quarter
     would be far outside that."""
-    from glsdm.layers.common import linear
+    from glsdm import _native as NT
     g = torch.Generator().manual_seed(M * 7 + N + K)
     lin = torch.nn.Linear(K, N, bias=bias).to(device=device, dtype=torch.bfloat16)
     with torch.no_grad():
@@ -160,7 +160,9 @@ def test_linear_small_matches_float64_and_torch(device, M, N, K, bias):
             lin.bias.copy_((torch.randn(N, generator=g) * 0.5).to(device))
     x = torch.randn(M, K, generator=g).to(device=device, dtype=torch.bfloat16)
     with torch.no_grad():
-        out = linear(lin, x)
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+        NT.call("glsdm_linear_small", NT.ptr(x), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(out), M, N, K,
+                NT.stream(device))
         ref_torch = torch.nn.functional.linear(x, lin.weight, lin.bias)
     ref = x.double().cpu() @ lin.weight.double().cpu().T
     if bias:
@@ -173,11 +175,23 @@ def test_linear_small_matches_float64_and_torch(device, M, N, K, bias):
     assert (out == ref_torch).float().mean().item() > 0.9
 
 
-def test_linear_small_falls_back_for_other_shapes(device):
-    """Inputs the kernel does not take (more than 64 rows, K not a multiple of 128,
-    fp32, under autograd) go through torch's linear unchanged."""
+def test_linear_routes_decode_projections(device):
+    """The stack's ``linear``: decode-sized projections run the kernel (its bits, not
+    necessarily torch's); more rows, other widths and autograd go through torch's
+    linear unchanged."""
+    from glsdm import _native as NT
     from glsdm.layers.common import linear
-    lin = torch.nn.Linear(96, 32).to(device=device, dtype=torch.bfloat16)
-    x = torch.randn(65, 96, device=device, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(5)
+    lin = torch.nn.Linear(1024, 3072).to(device=device, dtype=torch.bfloat16)
+    x = torch.randn(64, 1024, generator=g).to(device=device, dtype=torch.bfloat16)
     with torch.no_grad():
+        direct = torch.empty(64, 3072, dtype=torch.bfloat16, device=device)
+        NT.call("glsdm_linear_small", NT.ptr(x), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(direct), 64, 3072,
+                1024, NT.stream(device))
+        assert torch.equal(linear(lin, x), direct)
+        for shape, n_out, k_in in (((65, 1024), 3072, 1024), ((64, 96), 32, 96), ((64, 1024), 40, 1024)):
+            other = torch.nn.Linear(k_in, n_out).to(device=device, dtype=torch.bfloat16)
+            y = torch.randn(*shape, generator=g).to(device=device, dtype=torch.bfloat16)
+            assert torch.equal(linear(other, y), other(y))
+    with torch.enable_grad():
         assert torch.equal(linear(lin, x), lin(x))
