@@ -23,21 +23,30 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 constexpr int LS_MAX_ROWS = 64;
 
-__global__ __launch_bounds__(256) void linear_small_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
+// CT column tiles of 16 per block: each wave multiplies its x fragments into CT
+// weight tiles, so wide projections (2^15 columns) read x from L2 CT times less.
+// W waves split K (16 for deep reductions: each wave's chain of dependent k-steps
+// stays at 8 for K = 4096).
+template <int CT, int W>
+__global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
                                                            const bf16_t *__restrict__ bias, bf16_t *__restrict__ out,
                                                            int M, int N, int K)
 {
 #pragma clang fp contract(off)
-    __shared__ float s_part[4][LS_MAX_ROWS][17];
+    __shared__ float s_part[W][LS_MAX_ROWS][16 * CT + 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int li = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const int kw = K / 4;                     // this wave's K range [wave * kw, wave * kw + kw)
+    const int n0 = blockIdx.x * 16 * CT;
+    const int kw = K / W;                     // this wave's K range [wave * kw, wave * kw + kw)
     const int RT = (M + 15) / 16;             // row tiles (block-uniform)
-    const bf16_t *wrow = w + (int64_t)(n0 + li) * K + wave * kw + kq * 8;
-    floatx4_t acc[4];
+    const bf16_t *wrow[CT];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) acc[rt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < CT; ++ct) wrow[ct] = w + (int64_t)(n0 + 16 * ct + li) * K + wave * kw + kq * 8;
+    floatx4_t acc[4][CT];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4_t{0.f, 0.f, 0.f, 0.f};
     // row li of tile rt; rows past M read row M - 1 and are never stored
     const bf16_t *xrow[4];
 #pragma unroll
@@ -46,28 +55,35 @@ __global__ __launch_bounds__(256) void linear_small_kernel(const bf16_t *__restr
         xrow[rt] = x + (int64_t)m * K + wave * kw + kq * 8;
     }
     for (int k0 = 0; k0 < kw; k0 += 32) {
-        const bf16x8_t b = *reinterpret_cast<const bf16x8_t *>(wrow + k0);
+        bf16x8_t b[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) b[ct] = *reinterpret_cast<const bf16x8_t *>(wrow[ct] + k0);
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             if (rt < RT) {
                 const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(xrow[rt] + k0);
-                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[rt], 0, 0, 0);
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct)
+                    acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[ct], acc[rt][ct], 0, 0, 0);
             }
         }
     }
-    // acc[rt][i]: row rt*16 + 4*kq + i, column n0 + li
+    // acc[rt][ct][i]: row rt*16 + 4*kq + i, column n0 + 16 ct + li
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
         if (rt < RT)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s_part[wave][rt * 16 + 4 * kq + i][li] = acc[rt][i];
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s_part[wave][rt * 16 + 4 * kq + i][16 * ct + li] = acc[rt][ct][i];
     __syncthreads();
-    for (int e = threadIdx.x; e < RT * 16 * 16; e += 256) {
-        const int m = e >> 4, c = e & 15;
+    // the W partial tiles summed in wave order, then the bias, then one rounding
+    for (int e = threadIdx.x; e < RT * 16 * 16 * CT; e += 64 * W) {
+        const int m = e / (16 * CT), c = e % (16 * CT);
         if (m < M) {
-            float s = s_part[0][m][c] + s_part[1][m][c];
-            s = s + s_part[2][m][c];
-            s = s + s_part[3][m][c];
+            float s = s_part[0][m][c];
+#pragma unroll
+            for (int q = 1; q < W; ++q) s = s + s_part[q][m][c];
             if (bias) s = s + bf16_to_f32(bias[n0 + c]);
             out[(int64_t)m * N + n0 + c] = f32_to_bf16(s);
         }
@@ -87,8 +103,20 @@ extern "C" int glsdm_linear_small(const void *x, const void *weight, const void 
     if (!x || !weight || !out) return fail(GLSDM_ERR_ARG, "linear_small: null pointer");
     if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) != 0)
         return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: x and weight must be 16-byte aligned");
-    hipLaunchKernelGGL(linear_small_kernel, dim3((unsigned)(N / 16)), dim3(256), 0, as_stream(stream),
-                       static_cast<const bf16_t *>(x), static_cast<const bf16_t *>(weight),
-                       static_cast<const bf16_t *>(bias), static_cast<bf16_t *>(out), (int)M, (int)N, (int)K);
+    const bf16_t *xx = static_cast<const bf16_t *>(x), *ww = static_cast<const bf16_t *>(weight);
+    const bf16_t *bb = static_cast<const bf16_t *>(bias);
+    bf16_t *oo = static_cast<bf16_t *>(out);
+    // four column tiles per block for wide projections (still >= 256 blocks), one otherwise;
+    // sixteen waves over K for deep reductions
+    hipStream_t st = as_stream(stream);
+    if (N % 64 == 0 && N >= 16384)
+        hipLaunchKernelGGL((linear_small_kernel<4, 4>), dim3((unsigned)(N / 64)), dim3(256), 0, st, xx, ww, bb, oo,
+                           (int)M, (int)N, (int)K);
+    else if (K >= 4096 && K % (16 * 32) == 0)
+        hipLaunchKernelGGL((linear_small_kernel<1, 16>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, xx, ww, bb, oo,
+                           (int)M, (int)N, (int)K);
+    else
+        hipLaunchKernelGGL((linear_small_kernel<1, 4>), dim3((unsigned)(N / 16)), dim3(256), 0, st, xx, ww, bb, oo,
+                           (int)M, (int)N, (int)K);
     return check_launch("linear_small_kernel");
 }

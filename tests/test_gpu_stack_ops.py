@@ -143,7 +143,8 @@ def test_write_gates_match_tensor_ops(device, dtype):
     (64, 3072, 1024, True),        # the config-5 decode projections: 64 streams x one token
     (64, 16, 1024, True),          # a write-gate projection (one column tile)
     (17, 1024, 4096, True),        # ragged rows, a long reduction (the MLP's down projection)
-    (1, 32000, 1024, False),       # one row through the vocabulary head (no bias)
+    (1, 32000, 1024, False),       # one row through the vocabulary head (no bias; four column tiles per block)
+    (64, 16384, 1024, True),       # a router score projection's width: four column tiles per block
     (40, 48, 128, True),           # the smallest reduction
 ])
 def test_linear_small_matches_float64_and_torch(device, M, N, K, bias):
