@@ -1,7 +1,8 @@
 // The stack's bf16 projections for decode-sized inputs (at most 64 rows) on gfx950.
 //
-// Semantics: torch.nn.functional.linear in bf16 (S/layers/*.py: every nn.Linear
-// of the stack), out[m, n] = bf16(sum_k x[m, k] * w[n, k] + bias[n]): bf16
+// Semantics: torch.nn.functional.linear in bf16 (every nn.Linear of the stack:
+// S/layers/attention.py:23-26, S/layers/common.py:22-23, S/layers/router.py:23-28,
+// S/model.py:45), out[m, n] = bf16(sum_k x[m, k] * w[n, k] + bias[n]): bf16
 // products accumulated in fp32 and rounded once, round-to-nearest-even.  The
 // fp32 summation order is this kernel's (the library GEMM's order is its own),
 // so results agree with torch's to the rounding of the fp32 sum.

@@ -53,6 +53,23 @@ _MASKS = {}
 APPEND_MAX_TOKENS = 16    # calls of at most this many tokens (decode) append to the KV window in place
 
 
+def decode_attention(q, k, v):
+    """``F.scaled_dot_product_attention(q, k, v)`` for one query row per (request,
+    head), ``q [B, H, 1, dk]`` contiguous bf16, ``k``/``v [B, H, L, dk]`` strided
+    views with unit last stride, no mask (``glsdm_decode_attention``: fp32 scores,
+    softmax and sums, rounded once; within rounding of the library's kernel)."""
+    B, H, _, dk = q.shape
+    L = k.shape[2]
+    if k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise ValueError("decode_attention needs unit-stride key and value rows")
+    out = torch.empty_like(q)
+    ks = (ctypes.c_int64 * 3)(*k.stride()[:3])
+    vs = (ctypes.c_int64 * 3)(*v.stride()[:3])
+    N.call("glsdm_decode_attention", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(out), B, H, L, dk, ks, vs,
+           ctypes.c_float(dk ** -0.5), N.stream(q.device))
+    return out
+
+
 def _window_mask(previous, T, window, device, dtype):
     """Query i (position offset + i) may see key j (position offset - previous + j)
     when the key is not later and, with a window, less than ``window`` back.  It
@@ -192,10 +209,17 @@ class Transformer(nn.Module):
             k, v = k.repeat_interleave(groups, 1), v.repeat_interleave(groups, 1)
         # keys cover positions [offset - previous, offset + T); a cached prefill
         # needs this offset causal mask (SDPA's own causal mask is upper-left aligned)
-        mask = None
-        if offset or self.window is not None:
-            mask = _window_mask(previous, T, self.window, x.device, q.dtype)
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
+        if (T == 1 and fused and groups == 1 and q.dtype == torch.bfloat16 and dk in (64, 128) and k.shape[2] <= 1024
+                and (self.window is None or previous < self.window) and q.is_contiguous()
+                and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad))):
+            # one token per request with every cached key inside its window (the mask is
+            # all zeros): one HIP launch instead of the library's attention
+            out = decode_attention(q, k, v)
+        else:
+            mask = None
+            if offset or self.window is not None:
+                mask = _window_mask(previous, T, self.window, x.device, q.dtype)
+            out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
         if fused and out.stride(-1) == 1 and gate.stride(-1) == 1 and not (
                 torch.is_grad_enabled() and (out.requires_grad or gate.requires_grad)):
             return linear(self.proj, gate_merge(out, gate))

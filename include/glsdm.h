@@ -503,12 +503,26 @@ int glsdm_relu2_gate(const void *fc, int32_t dtype, int64_t rows, int64_t inner,
  * (GLSDM_ERR_UNSUPPORTED otherwise, nothing launched).  The fp32 summation order
  * is the kernel's own: results agree with torch's bf16 linear to the rounding of
  * the fp32 sum.
- * Replaces: the nn.Linear projections of S/layers/attention.py:11-42,
- * S/layers/common.py:21-27, S/layers/router.py:13-36 and the head of
- * S/model.py:84-96 for decode-sized inputs (torch.nn.functional.linear).
+ * Replaces: the nn.Linear projections of S/layers/attention.py:23-26,
+ * S/layers/common.py:22-23, S/layers/router.py:23-28 and the head of
+ * S/model.py:45 for decode-sized inputs (torch.nn.functional.linear).
  */
 int glsdm_linear_small(const void *x, const void *weight, const void *bias, void *out, int64_t M, int64_t N,
                        int64_t K, void *stream);
+
+/*
+ * One-token attention of the local layer's decode step, bf16:
+ *   out [B, H, 1, dk] = softmax(q . k_j * scale) . v_j over the L keys of each
+ *   (b, h), q [B, H, 1, dk] contiguous, k/v [B, H, L, dk] read through
+ *   k_strides/v_strides (elements, for the b, h and key dimensions; unit stride
+ *   within a row).  fp32 scores, exponentials and sums, the output rounded once.
+ * No mask: for one query whose keys all lie inside its window.  L <= 1024,
+ * dk 64 or 128, q and key rows 16-byte aligned (GLSDM_ERR_UNSUPPORTED otherwise).
+ * Replaces: F.scaled_dot_product_attention of S/layers/attention.py:76 for a
+ * decode step (T = 1).
+ */
+int glsdm_decode_attention(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H, int64_t L,
+                           int64_t dk, const int64_t *k_strides, const int64_t *v_strides, float scale, void *stream);
 
 /*
  * RMSNorm then a cast: per row of x [rows, dim] (x_dtype), r =

@@ -196,3 +196,33 @@ def test_linear_routes_decode_projections(device):
             assert torch.equal(linear(other, y), other(y))
     with torch.enable_grad():
         assert torch.equal(linear(lin, x), lin(x))
+
+
+@pytest.mark.parametrize("B,H,L,dk", [
+    (64, 16, 512, 64),             # config 5: a full window of 511 cached keys and the new one
+    (3, 2, 1, 64),                 # the first decode step after an empty cache: one key
+    (2, 4, 77, 128),               # a ragged key count, wider heads
+    (1, 1, 1024, 64),              # the kernel's largest key count
+])
+def test_decode_attention_matches_sdpa(device, B, H, L, dk):
+    """glsdm_decode_attention on strided views of a KV buffer (as the cache holds
+    them) against PyTorch's SDPA of the same bf16 operands computed in fp32: within
+    bf16 rounding of the output; and against SDPA itself on bf16."""
+    from glsdm.layers.attention import decode_attention
+    g = torch.Generator().manual_seed(B * 1000 + L + dk)
+    q = torch.randn(B, H, 1, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    buf_k = torch.randn(B, H, L + 40, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    buf_v = torch.randn(B, H, L + 40, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    k, v = buf_k[:, :, 7:7 + L], buf_v[:, :, 7:7 + L]      # views inside a larger buffer
+    with torch.no_grad():
+        out = decode_attention(q, k, v)
+        ref32 = F.scaled_dot_product_attention(q.float(), k.float(), v.float())
+        ref16 = F.scaled_dot_product_attention(q, k.contiguous(), v.contiguous())
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    torch.testing.assert_close(out.float(), ref32, rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(out.float(), ref16.float(), rtol=2e-2, atol=2e-2)
+    # a planted slip -- the value rows read one key late -- is far outside that
+    with torch.no_grad():
+        slip = decode_attention(q, buf_k[:, :, 7:7 + L], buf_v[:, :, 8:8 + L])
+    if L > 1:
+        assert (slip.float() - ref32).abs().max() > 5e-2
