@@ -54,6 +54,19 @@ def _proposal_log(model, cache, batch, chunk):
     return cache.log
 
 
+def _all_logged(cache):
+    """Whether every pending proposal of the cache is a ``LoggedProposal``.  The answer
+    is kept with the pending tuple it was computed for (tuples are immutable, so the
+    same object has the same contents): a decode step would otherwise walk the
+    chunk's thousands of pending proposals every time."""
+    memo = getattr(cache, "_all_logged", None)
+    if memo is not None and memo[0] is cache.pending:
+        return memo[1]
+    flag = all(isinstance(p, LoggedProposal) for p in cache.pending)
+    cache._all_logged = (cache.pending, flag)
+    return flag
+
+
 def forward(model, inputs, cache=None):
     """Run embedded ``inputs [B, T, dim]`` through the stack; returns
     ``(hidden [B, T, dim], reg, align)``.  ``cache`` is a request cache
@@ -70,7 +83,7 @@ def forward(model, inputs, cache=None):
     # proposal log: inference on the device, and no pending proposal of another kind
     use_log = (model.cfg.get("gl_proposal_log", True) and not torch.is_grad_enabled() and cache.view.values.is_cuda
                and any(isinstance(b, GlobalLayer) for b in model.blocks)
-               and all(isinstance(p, LoggedProposal) for p in cache.pending))
+               and _all_logged(cache))
     outputs = []
     reg, align = inputs.new_zeros(()), inputs.new_zeros(())
     position = 0
@@ -98,7 +111,9 @@ def forward(model, inputs, cache=None):
             if cache.log is not None:
                 cache.log.clear()          # its rows are committed: the next chunk reuses them
         else:
+            logged = _all_logged(cache) and all(isinstance(p, LoggedProposal) for p in proposals[len(cache.pending):])
             cache.pending = tuple(proposals)
+            cache._all_logged = (cache.pending, logged)
         outputs.append(x)
         position += length
     return torch.cat(outputs, 1), reg / layers, align / layers
