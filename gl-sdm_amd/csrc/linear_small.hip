@@ -15,6 +15,8 @@
 // up to four 16-row tiles (fragments loaded straight from L2/HBM: x is shared by
 // every block, each weight row is read once), then the four partial tiles are
 // summed in a fixed order through LDS and the bias is added before the rounding.
+// Projections of one input (a layer's q, k and v) can share one launch: the grid
+// is their column tiles side by side, each block picks its projection by index.
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -23,21 +25,47 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 constexpr int LS_MAX_ROWS = 64;
+constexpr int LS_MAX_GROUP = 8;
+
+// the projections of one launch (passed by value): projection i owns blocks
+// [first[i], first[i + 1]) and writes out[i] [M, N[i]]
+struct LinearGroup {
+    const bf16_t *w[LS_MAX_GROUP];
+    const bf16_t *bias[LS_MAX_GROUP];
+    bf16_t *out[LS_MAX_GROUP];
+    int N[LS_MAX_GROUP];
+    int first[LS_MAX_GROUP + 1];
+    int count;
+};
 
 // CT column tiles of 16 per block: each wave multiplies its x fragments into CT
 // weight tiles, so wide projections (2^15 columns) read x from L2 CT times less.
 // W waves split K (16 for deep reductions: each wave's chain of dependent k-steps
 // stays at 8 for K = 4096).
 template <int CT, int W>
-__global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__restrict__ x, const bf16_t *__restrict__ w,
-                                                           const bf16_t *__restrict__ bias, bf16_t *__restrict__ out,
-                                                           int M, int N, int K)
+__global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__restrict__ x, const LinearGroup g, int M,
+                                                           int K)
 {
 #pragma clang fp contract(off)
     __shared__ float s_part[W][LS_MAX_ROWS][16 * CT + 1];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int li = lane & 15, kq = lane >> 4;
-    const int n0 = blockIdx.x * 16 * CT;
+    // this block's projection, chosen with constant indices only (a runtime index
+    // into the argument struct would copy it to scratch memory)
+    const bf16_t *__restrict__ w = g.w[0];
+    const bf16_t *__restrict__ bias = g.bias[0];
+    bf16_t *__restrict__ out = g.out[0];
+    int N = g.N[0], base = 0;
+#pragma unroll
+    for (int i = 1; i < LS_MAX_GROUP; ++i)
+        if (i < g.count && (int)blockIdx.x >= g.first[i]) {
+            w = g.w[i];
+            bias = g.bias[i];
+            out = g.out[i];
+            N = g.N[i];
+            base = g.first[i];
+        }
+    const int n0 = ((int)blockIdx.x - base) * 16 * CT;
     const int kw = K / W;                     // this wave's K range [wave * kw, wave * kw + kw)
     const int RT = (M + 15) / 16;             // row tiles (block-uniform)
     const bf16_t *wrow[CT];
@@ -95,29 +123,87 @@ __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__re
 
 using namespace glsdm;
 
+namespace {
+
+// CT = 4 for wide projections (still >= 256 blocks each), 1 otherwise; W = 16 waves
+// over K for deep reductions.  W fixes the summation order; CT does not.
+int launch_group(const bf16_t *x, LinearGroup &g, int M, int K, bool wide, hipStream_t st)
+{
+    const int CT = wide ? 4 : 1;
+    g.first[0] = 0;
+    for (int i = 0; i < g.count; ++i) g.first[i + 1] = g.first[i] + g.N[i] / (16 * CT);
+    for (int i = g.count + 1; i <= LS_MAX_GROUP; ++i) g.first[i] = g.first[g.count];
+    const dim3 grid((unsigned)g.first[g.count]);
+    if (wide)
+        hipLaunchKernelGGL((linear_small_kernel<4, 4>), grid, dim3(256), 0, st, x, g, M, K);
+    else if (K >= 4096 && K % (16 * 32) == 0)
+        hipLaunchKernelGGL((linear_small_kernel<1, 16>), grid, dim3(1024), 0, st, x, g, M, K);
+    else
+        hipLaunchKernelGGL((linear_small_kernel<1, 4>), grid, dim3(256), 0, st, x, g, M, K);
+    return check_launch("linear_small_kernel");
+}
+
+int check_shape(const void *x, int64_t M, int64_t K)
+{
+    if (M < 1 || K < 1) return fail(GLSDM_ERR_ARG, "linear_small: bad shape");
+    if (M > LS_MAX_ROWS || K % 128 != 0 || K > 0x7FFFFFFF)
+        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: M <= 64, N a multiple of 16 and K of 128 required");
+    if (!x) return fail(GLSDM_ERR_ARG, "linear_small: null pointer");
+    if ((reinterpret_cast<uintptr_t>(x) & 15) != 0)
+        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: x and weight must be 16-byte aligned");
+    return GLSDM_OK;
+}
+
+int check_projection(const void *weight, const void *out, int64_t N)
+{
+    if (N < 1) return fail(GLSDM_ERR_ARG, "linear_small: bad shape");
+    if (N % 16 != 0 || N > 0x7FFFFFF0)
+        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: M <= 64, N a multiple of 16 and K of 128 required");
+    if (!weight || !out) return fail(GLSDM_ERR_ARG, "linear_small: null pointer");
+    if ((reinterpret_cast<uintptr_t>(weight) & 15) != 0)
+        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: x and weight must be 16-byte aligned");
+    return GLSDM_OK;
+}
+
+}  // namespace
+
 extern "C" int glsdm_linear_small(const void *x, const void *weight, const void *bias, void *out, int64_t M,
                                   int64_t N, int64_t K, void *stream)
 {
-    if (M < 1 || N < 1 || K < 1) return fail(GLSDM_ERR_ARG, "linear_small: bad shape");
-    if (M > LS_MAX_ROWS || N % 16 != 0 || K % 128 != 0 || N > (int64_t)16 * 0x7FFFFFFF || K > 0x7FFFFFFF)
-        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: M <= 64, N a multiple of 16 and K of 128 required");
-    if (!x || !weight || !out) return fail(GLSDM_ERR_ARG, "linear_small: null pointer");
-    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight)) & 15) != 0)
-        return fail(GLSDM_ERR_UNSUPPORTED, "linear_small: x and weight must be 16-byte aligned");
-    const bf16_t *xx = static_cast<const bf16_t *>(x), *ww = static_cast<const bf16_t *>(weight);
-    const bf16_t *bb = static_cast<const bf16_t *>(bias);
-    bf16_t *oo = static_cast<bf16_t *>(out);
-    // four column tiles per block for wide projections (still >= 256 blocks), one otherwise;
-    // sixteen waves over K for deep reductions
-    hipStream_t st = as_stream(stream);
-    if (N % 64 == 0 && N >= 16384)
-        hipLaunchKernelGGL((linear_small_kernel<4, 4>), dim3((unsigned)(N / 64)), dim3(256), 0, st, xx, ww, bb, oo,
-                           (int)M, (int)N, (int)K);
-    else if (K >= 4096 && K % (16 * 32) == 0)
-        hipLaunchKernelGGL((linear_small_kernel<1, 16>), dim3((unsigned)(N / 16)), dim3(1024), 0, st, xx, ww, bb, oo,
-                           (int)M, (int)N, (int)K);
-    else
-        hipLaunchKernelGGL((linear_small_kernel<1, 4>), dim3((unsigned)(N / 16)), dim3(256), 0, st, xx, ww, bb, oo,
-                           (int)M, (int)N, (int)K);
-    return check_launch("linear_small_kernel");
+    int rc = check_shape(x, M, K);
+    if (rc == GLSDM_OK) rc = check_projection(weight, out, N);
+    if (rc != GLSDM_OK) return rc;
+    LinearGroup g{};
+    g.count = 1;
+    g.w[0] = static_cast<const bf16_t *>(weight);
+    g.bias[0] = static_cast<const bf16_t *>(bias);
+    g.out[0] = static_cast<bf16_t *>(out);
+    g.N[0] = (int)N;
+    return launch_group(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
+                        as_stream(stream));
+}
+
+extern "C" int glsdm_linear_small_group(const void *x, int32_t count, const void *const *weights,
+                                        const void *const *biases, void *const *outs, const int64_t *N, int64_t M,
+                                        int64_t K, void *stream)
+{
+    int rc = check_shape(x, M, K);
+    if (rc != GLSDM_OK) return rc;
+    if (count < 1 || count > LS_MAX_GROUP) return fail(GLSDM_ERR_ARG, "linear_small_group: 1 to 8 projections");
+    if (!weights || !outs || !N) return fail(GLSDM_ERR_ARG, "linear_small_group: null pointer");
+    LinearGroup g{};
+    g.count = count;
+    bool wide = true;
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if ((rc = check_projection(weights[i], outs[i], N[i])) != GLSDM_OK) return rc;
+        g.w[i] = static_cast<const bf16_t *>(weights[i]);
+        g.bias[i] = biases ? static_cast<const bf16_t *>(biases[i]) : nullptr;
+        g.out[i] = static_cast<bf16_t *>(outs[i]);
+        g.N[i] = (int)N[i];
+        wide = wide && N[i] % 64 == 0 && N[i] >= 16384;
+        blocks += N[i] / 16;
+    }
+    if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "linear_small_group: too many columns");
+    return launch_group(static_cast<const bf16_t *>(x), g, (int)M, (int)K, wide, as_stream(stream));
 }

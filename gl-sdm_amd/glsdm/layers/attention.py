@@ -21,7 +21,7 @@ from torch import nn
 import torch.nn.functional as F
 
 from .. import _native as N
-from .common import linear
+from .common import linear, linear_group
 
 
 def qk_norm_rotary(x, freq, offset):
@@ -175,9 +175,10 @@ class Transformer(nn.Module):
     def forward(self, x, cache=None):
         B, T, D = x.shape
         dk = self.head_dim
-        q, gate = linear(self.q, x).view(B, T, self.num_heads, 2 * dk).chunk(2, -1)
-        k = linear(self.k, x).view(B, T, self.num_kv_heads, dk)
-        v = linear(self.v, x).view(B, T, self.num_kv_heads, dk).transpose(1, 2)
+        q, k, v = linear_group((self.q, self.k, self.v), x)
+        q, gate = q.view(B, T, self.num_heads, 2 * dk).chunk(2, -1)
+        k = k.view(B, T, self.num_kv_heads, dk)
+        v = v.view(B, T, self.num_kv_heads, dk).transpose(1, 2)
         previous = cache["k"].shape[2] if cache and cache.get("k") is not None else 0
         offset = 0 if cache is None else cache.get("tokens", previous)
         fused = (x.is_cuda and dk in (4, 8, 16, 32, 64, 128, 256) and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24

@@ -17,20 +17,48 @@ def linear(layer, x):
     as torch's bf16 linear, in the kernel's own summation order (results agree to
     the rounding of the fp32 sum).  A decode step makes over a hundred of these
     calls; the library GEMM's host cost per call (~20 us) is what bounds that step."""
-    w = layer.weight
-    K = x.shape[-1]
     # every eligible shape: alone, the router's 2^15-column score projection takes 41 us here
     # against the library's ~20 us per call, but within a decode step the library's host
     # time costs more (config 5 p50 4.02 ms when such projections go to the library, 3.77 ms)
-    if (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
-            and x.numel() <= 64 * K and w.shape[0] % 16 == 0 and K % 128 == 0 and x.is_contiguous()
-            and x.data_ptr() % 16 == 0 and w.is_contiguous()
-            and (layer.bias is None or layer.bias.dtype == torch.bfloat16)):
+    if _small(layer, x):
+        K = x.shape[-1]
+        w = layer.weight
         out = torch.empty((*x.shape[:-1], w.shape[0]), dtype=torch.bfloat16, device=x.device)
         N.call("glsdm_linear_small", N.ptr(x), N.ptr(w), N.ptr(layer.bias), N.ptr(out), x.numel() // K, w.shape[0],
                K, N.stream(x.device))
         return out
     return layer(x)
+
+
+def _small(layer, x):
+    w = layer.weight
+    K = x.shape[-1]
+    return (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+            and x.numel() <= 64 * K and w.shape[0] % 16 == 0 and K % 128 == 0 and x.is_contiguous()
+            and x.data_ptr() % 16 == 0 and w.is_contiguous() and w.device == x.device
+            and (layer.bias is None or layer.bias.dtype == torch.bfloat16))
+
+
+def linear_group(layers, x):
+    """``[linear(l, x) for l in layers]``; when every projection is eligible for
+    ``glsdm_linear_small``, one launch of ``glsdm_linear_small_group`` computes them
+    all (bit-identical to the separate calls: the outputs are contiguous pieces of
+    one buffer)."""
+    if not 1 < len(layers) <= 8 or not all(_small(l, x) for l in layers):
+        return [linear(l, x) for l in layers]
+    K, M = x.shape[-1], x.numel() // x.shape[-1]
+    widths = [l.weight.shape[0] for l in layers]
+    flat = torch.empty(M * sum(widths), dtype=torch.bfloat16, device=x.device)
+    outs, at = [], 0
+    for n in widths:
+        outs.append(flat[at:at + M * n].view(*x.shape[:-1], n))
+        at += M * n
+    count = len(layers)
+    P = N.ctypes.c_void_p
+    N.call("glsdm_linear_small_group", N.ptr(x), count, (P * count)(*(l.weight.data_ptr() for l in layers)),
+           (P * count)(*(0 if l.bias is None else l.bias.data_ptr() for l in layers)),
+           (P * count)(*(o.data_ptr() for o in outs)), (N.ctypes.c_int64 * count)(*widths), M, K, N.stream(x.device))
+    return outs
 
 
 def relu2_gate(h):

@@ -9,7 +9,7 @@ from .. import _native as N
 from ..memory import routing
 from ..memory.proposals import layer_proposal, log_proposal
 from .block import check_reg_mode, regulariser, zero
-from .common import MLP, RMSNorm, linear
+from .common import MLP, RMSNorm, linear, linear_group
 from .router import GlobalRouter
 
 
@@ -70,8 +70,8 @@ class GlobalLayer(nn.Module):
         prediction, index, weights = routing.routed_read(self, snapshot.values, scores, router.num_writes, physical)
         vdt = router.v.weight.dtype
         dense = zk if vdt == zk.dtype else self.norm1.cast(x, vdt)
-        target = linear(router.v, dense).view(B, T, router.heads, router.head_dim)
-        b_lin, d_lin = linear(router.beta, dense), linear(router.decay, dense)
+        target, b_lin, d_lin = linear_group((router.v, router.beta, router.decay), dense)
+        target = target.view(B, T, router.heads, router.head_dim)
         if log is not None and not training and b_lin.is_cuda and b_lin.dtype in (torch.float32, torch.bfloat16):
             return log_proposal(log, snapshot, index, weights, prediction, target, b_lin, d_lin, offset, layer_idx,
                                 chunk_size, num_layers)

@@ -511,6 +511,18 @@ int glsdm_linear_small(const void *x, const void *weight, const void *bias, void
                        int64_t K, void *stream);
 
 /*
+ * glsdm_linear_small for up to 8 projections of one input in one launch:
+ *   outs[i] [M, N[i]] = bf16(x . weights[i]^T + biases[i]), i < count,
+ * each with glsdm_linear_small's requirements and bit-identical to it (biases may
+ * be NULL, or any biases[i] NULL).
+ * Replaces: the projections of one input, S/layers/attention.py:23-25 (q, k, v of
+ * a local layer) and S/layers/router.py:25-27 (v, beta, decay of a global layer's
+ * write), for decode-sized inputs.
+ */
+int glsdm_linear_small_group(const void *x, int32_t count, const void *const *weights, const void *const *biases,
+                             void *const *outs, const int64_t *N, int64_t M, int64_t K, void *stream);
+
+/*
  * One-token attention of the local layer's decode step, bf16:
  *   out [B, H, 1, dk] = softmax(q . k_j * scale) . v_j over the L keys of each
  *   (b, h), q [B, H, 1, dk] contiguous, k/v [B, H, L, dk] read through

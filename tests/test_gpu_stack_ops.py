@@ -198,6 +198,49 @@ def test_linear_routes_decode_projections(device):
         assert torch.equal(linear(lin, x), lin(x))
 
 
+@pytest.mark.parametrize("M,widths,K,biases", [
+    (64, (2048, 1024, 1024), 1024, (True, True, True)),     # a local layer's q, k, v (config 5 decode)
+    (64, (1024, 16, 16), 1024, (True, True, True)),         # a global layer's v, beta, decay
+    (17, (48, 1024, 32), 4096, (True, False, True)),        # ragged rows, a long reduction, one bias missing
+    (3, (16384, 32768), 256, (False, False)),               # wide projections: four column tiles per block
+    (1, tuple(16 * (i + 1) for i in range(8)), 128, (True,) * 8),   # the most projections per launch
+])
+def test_linear_small_group_equals_separate_calls(device, M, widths, K, biases):
+    """glsdm_linear_small_group: each projection's output bit-identical to its own
+    glsdm_linear_small call (the same summation order), and within a bf16 rounding
+    of the float64 product (a projection reading its neighbour's weights or bias
+    would not be)."""
+    from glsdm import _native as NT
+    from glsdm.layers.common import linear_group
+    g = torch.Generator().manual_seed(M + K + len(widths))
+    layers = []
+    for n, b in zip(widths, biases):
+        lin = torch.nn.Linear(K, n, bias=b).to(device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_((torch.randn(n, K, generator=g) / K ** 0.5).to(device))
+            if b:
+                lin.bias.copy_((torch.randn(n, generator=g) * 0.5).to(device))
+        layers.append(lin)
+    x = torch.randn(M, K, generator=g).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        outs = linear_group(layers, x)
+        for lin, out in zip(layers, outs):
+            alone = torch.empty(M, lin.out_features, dtype=torch.bfloat16, device=device)
+            NT.call("glsdm_linear_small", NT.ptr(x), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(alone), M,
+                    lin.out_features, K, NT.stream(device))
+            assert out.shape == (M, lin.out_features) and out.is_contiguous()
+            assert torch.equal(out, alone)
+            ref = x.double().cpu() @ lin.weight.double().cpu().T
+            if lin.bias is not None:
+                ref = ref + lin.bias.double().cpu()
+            torch.testing.assert_close(out.double().cpu(), ref, rtol=8e-3, atol=1e-3 * ref.abs().max().item())
+    # an ineligible member (a width not a multiple of 16) sends every projection to torch
+    odd = torch.nn.Linear(K, 24).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        got = linear_group([layers[0], odd], x)
+    assert torch.equal(got[1], odd(x).detach())
+
+
 @pytest.mark.parametrize("B,H,L,dk", [
     (64, 16, 512, 64),             # config 5: a full window of 511 cached keys and the new one
     (3, 2, 1, 64),                 # the first decode step after an empty cache: one key
