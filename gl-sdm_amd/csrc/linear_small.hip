@@ -36,13 +36,17 @@ struct LinearGroup {
     int N[LS_MAX_GROUP];
     int first[LS_MAX_GROUP + 1];
     int count;
+    // residual form (one projection): res_out = residual + float(bf16 result)
+    const float *residual;
+    float *res_out;
 };
 
 // CT column tiles of 16 per block: each wave multiplies its x fragments into CT
 // weight tiles, so wide projections (2^15 columns) read x from L2 CT times less.
 // W waves split K (16 for deep reductions: each wave's chain of dependent k-steps
-// stays at 8 for K = 4096).
-template <int CT, int W>
+// stays at 8 for K = 4096).  RES: the residual form, whose rounded bf16 result is
+// added in fp32 to an fp32 residual (torch's x + y for fp32 x and bf16 y).
+template <int CT, int W, bool RES>
 __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__restrict__ x, const LinearGroup g, int M,
                                                            int K)
 {
@@ -114,7 +118,11 @@ __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__re
 #pragma unroll
             for (int q = 1; q < W; ++q) s = s + s_part[q][m][c];
             if (bias) s = s + bf16_to_f32(bias[n0 + c]);
-            out[(int64_t)m * N + n0 + c] = f32_to_bf16(s);
+            const int64_t o = (int64_t)m * N + n0 + c;
+            if constexpr (RES)
+                g.res_out[o] = g.residual[o] + bf16_to_f32(f32_to_bf16(s));
+            else
+                out[o] = f32_to_bf16(s);
         }
     }
 }
@@ -127,6 +135,7 @@ namespace {
 
 // CT = 4 for wide projections (still >= 256 blocks each), 1 otherwise; W = 16 waves
 // over K for deep reductions.  W fixes the summation order; CT does not.
+template <bool RES>
 int launch_group(const bf16_t *x, LinearGroup &g, int M, int K, bool wide, hipStream_t st)
 {
     const int CT = wide ? 4 : 1;
@@ -135,11 +144,11 @@ int launch_group(const bf16_t *x, LinearGroup &g, int M, int K, bool wide, hipSt
     for (int i = g.count + 1; i <= LS_MAX_GROUP; ++i) g.first[i] = g.first[g.count];
     const dim3 grid((unsigned)g.first[g.count]);
     if (wide)
-        hipLaunchKernelGGL((linear_small_kernel<4, 4>), grid, dim3(256), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<4, 4, RES>), grid, dim3(256), 0, st, x, g, M, K);
     else if (K >= 4096 && K % (16 * 32) == 0)
-        hipLaunchKernelGGL((linear_small_kernel<1, 16>), grid, dim3(1024), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<1, 16, RES>), grid, dim3(1024), 0, st, x, g, M, K);
     else
-        hipLaunchKernelGGL((linear_small_kernel<1, 4>), grid, dim3(256), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<1, 4, RES>), grid, dim3(256), 0, st, x, g, M, K);
     return check_launch("linear_small_kernel");
 }
 
@@ -179,8 +188,26 @@ extern "C" int glsdm_linear_small(const void *x, const void *weight, const void 
     g.bias[0] = static_cast<const bf16_t *>(bias);
     g.out[0] = static_cast<bf16_t *>(out);
     g.N[0] = (int)N;
-    return launch_group(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
-                        as_stream(stream));
+    return launch_group<false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
+                               as_stream(stream));
+}
+
+extern "C" int glsdm_linear_small_residual(const void *x, const void *weight, const void *bias, const float *residual,
+                                           float *out, int64_t M, int64_t N, int64_t K, void *stream)
+{
+    int rc = check_shape(x, M, K);
+    if (rc == GLSDM_OK) rc = check_projection(weight, out, N);
+    if (rc != GLSDM_OK) return rc;
+    if (!residual) return fail(GLSDM_ERR_ARG, "linear_small_residual: null pointer");
+    LinearGroup g{};
+    g.count = 1;
+    g.w[0] = static_cast<const bf16_t *>(weight);
+    g.bias[0] = static_cast<const bf16_t *>(bias);
+    g.N[0] = (int)N;
+    g.residual = residual;
+    g.res_out = out;
+    return launch_group<true>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
+                              as_stream(stream));
 }
 
 extern "C" int glsdm_linear_small_group(const void *x, int32_t count, const void *const *weights,
@@ -205,5 +232,5 @@ extern "C" int glsdm_linear_small_group(const void *x, int32_t count, const void
         blocks += N[i] / 16;
     }
     if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "linear_small_group: too many columns");
-    return launch_group(static_cast<const bf16_t *>(x), g, (int)M, (int)K, wide, as_stream(stream));
+    return launch_group<false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, wide, as_stream(stream));
 }

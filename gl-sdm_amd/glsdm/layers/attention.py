@@ -172,7 +172,7 @@ class Transformer(nn.Module):
                      vbuf=buf_v, end=end)
         return buf_k[:, :, start:end], buf_v[:, :, start:end]
 
-    def forward(self, x, cache=None):
+    def forward(self, x, cache=None, residual=None):
         B, T, D = x.shape
         dk = self.head_dim
         q, k, v = linear_group((self.q, self.k, self.v), x)
@@ -223,5 +223,5 @@ class Transformer(nn.Module):
             out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, is_causal=mask is None)
         if fused and out.stride(-1) == 1 and gate.stride(-1) == 1 and not (
                 torch.is_grad_enabled() and (out.requires_grad or gate.requires_grad)):
-            return linear(self.proj, gate_merge(out, gate))
-        return linear(self.proj, out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid())
+            return linear(self.proj, gate_merge(out, gate), residual)
+        return linear(self.proj, out.transpose(1, 2).reshape(B, T, D) * gate.reshape(B, T, D).sigmoid(), residual)

@@ -51,6 +51,6 @@ class Block(nn.Module):
 
     def forward(self, x, cache=None):
         dtype = self.mlp.fc.weight.dtype
-        x = x + self.attn(self.norm1.cast(x, dtype), cache=cache)
-        x = x + self.mlp(self.norm2.cast(x, dtype))
+        x = self.attn(self.norm1.cast(x, dtype), cache=cache, residual=x)
+        x = self.mlp(self.norm2.cast(x, dtype), residual=x)
         return x, regulariser(x, self.reg_mode), zero(x)

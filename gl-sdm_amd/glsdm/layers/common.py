@@ -10,24 +10,34 @@ import torch.nn.functional as F
 from .. import _native as N
 
 
-def linear(layer, x):
-    """``layer(x)`` for an ``nn.Linear``.  Outside autograd, a bf16 input of at most
-    64 rows on the device with a bf16 weight (out features a multiple of 16, in
-    features of 128) runs ``glsdm_linear_small``: fp32 accumulation rounded once,
-    as torch's bf16 linear, in the kernel's own summation order (results agree to
-    the rounding of the fp32 sum).  A decode step makes over a hundred of these
-    calls; the library GEMM's host cost per call (~20 us) is what bounds that step."""
+def linear(layer, x, residual=None):
+    """``layer(x)`` for an ``nn.Linear`` (``residual + layer(x)`` with a residual).
+    Outside autograd, a bf16 input of at most 64 rows on the device with a bf16
+    weight (out features a multiple of 16, in features of 128) runs
+    ``glsdm_linear_small``: fp32 accumulation rounded once, as torch's bf16 linear,
+    in the kernel's own summation order (results agree to the rounding of the fp32
+    sum); an fp32 residual of the output's shape is added in the same launch
+    (``glsdm_linear_small_residual``, the bits of torch's add).  A decode step makes
+    over a hundred of these calls; the library GEMM's host cost per call (~20 us) is
+    what bounds that step."""
     # every eligible shape: alone, the router's 2^15-column score projection takes 41 us here
     # against the library's ~20 us per call, but within a decode step the library's host
     # time costs more (config 5 p50 4.02 ms when such projections go to the library, 3.77 ms)
-    if _small(layer, x):
-        K = x.shape[-1]
-        w = layer.weight
-        out = torch.empty((*x.shape[:-1], w.shape[0]), dtype=torch.bfloat16, device=x.device)
-        N.call("glsdm_linear_small", N.ptr(x), N.ptr(w), N.ptr(layer.bias), N.ptr(out), x.numel() // K, w.shape[0],
-               K, N.stream(x.device))
+    if not _small(layer, x):
+        return layer(x) if residual is None else residual + layer(x)
+    K = x.shape[-1]
+    w = layer.weight
+    shape = (*x.shape[:-1], w.shape[0])
+    if (residual is not None and residual.dtype == torch.float32 and residual.is_contiguous()
+            and residual.device == x.device and tuple(residual.shape) == shape):
+        out = torch.empty(shape, dtype=torch.float32, device=x.device)
+        N.call("glsdm_linear_small_residual", N.ptr(x), N.ptr(w), N.ptr(layer.bias), N.ptr(residual), N.ptr(out),
+               x.numel() // K, w.shape[0], K, N.stream(x.device))
         return out
-    return layer(x)
+    out = torch.empty(shape, dtype=torch.bfloat16, device=x.device)
+    N.call("glsdm_linear_small", N.ptr(x), N.ptr(w), N.ptr(layer.bias), N.ptr(out), x.numel() // K, w.shape[0],
+           K, N.stream(x.device))
+    return out if residual is None else residual + out
 
 
 def _small(layer, x):
@@ -106,12 +116,14 @@ class MLP(nn.Module):
         self.fc = nn.Linear(dim, 2 * inner)
         self.proj = nn.Linear(inner, dim)
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """The MLP's output, or ``residual`` plus it (one launch with the projection
+        for a decode step)."""
         h = linear(self.fc, x)
         inner = h.shape[-1] // 2
         if (h.is_cuda and h.dtype in (torch.float32, torch.bfloat16) and h.is_contiguous()
                 and inner % (16 // h.element_size()) == 0 and h.data_ptr() % 16 == 0
                 and not (torch.is_grad_enabled() and h.requires_grad)):
-            return linear(self.proj, relu2_gate(h))
+            return linear(self.proj, relu2_gate(h), residual)
         u, gate = h.chunk(2, -1)
-        return linear(self.proj, gate * u.relu().square())
+        return linear(self.proj, gate * u.relu().square(), residual)

@@ -44,8 +44,8 @@ class GlobalLayer(nn.Module):
         dtype = router.q.weight.dtype
         scores = linear(router.q, self.norm1.cast(x, dtype)).view(B, T, router.heads, -1)
         readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
-        x = x + linear(router.proj, router.read_norm(readings.to(dtype)).flatten(-2))
-        x = x + self.mlp(self.norm2.cast(x, dtype))
+        x = linear(router.proj, router.read_norm(readings.to(dtype)).flatten(-2), x)
+        x = self.mlp(self.norm2.cast(x, dtype), residual=x)
         return x, regulariser(x, self.reg_mode), zero(x)
 
     def propose(self, x, snapshot, offset, layer_idx, chunk_size, num_layers, physical=None, log=None):

@@ -511,6 +511,18 @@ int glsdm_linear_small(const void *x, const void *weight, const void *bias, void
                        int64_t K, void *stream);
 
 /*
+ * glsdm_linear_small followed by the residual add, in one launch:
+ *   out [M, N] = residual [M, N] + float(bf16(x . weight^T + bias)), fp32, the
+ * bits of torch's x + linear(h) for an fp32 x and a bf16 projection; out may be
+ * residual itself.  Requirements as glsdm_linear_small.
+ * Replaces: the residual adds after the mixer and MLP projections,
+ * S/baselines/block.py:25-26 and S/layers/global_layer.py:29-30, for
+ * decode-sized inputs.
+ */
+int glsdm_linear_small_residual(const void *x, const void *weight, const void *bias, const float *residual,
+                                float *out, int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
  * glsdm_linear_small for up to 8 projections of one input in one launch:
  *   outs[i] [M, N[i]] = bf16(x . weights[i]^T + biases[i]), i < count,
  * each with glsdm_linear_small's requirements and bit-identical to it (biases may

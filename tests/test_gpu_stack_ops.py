@@ -198,6 +198,39 @@ def test_linear_routes_decode_projections(device):
         assert torch.equal(linear(lin, x), lin(x))
 
 
+@pytest.mark.parametrize("M,N,K", [
+    (64, 1024, 1024),              # a local layer's output projection (config 5 decode)
+    (64, 1024, 4096),              # the MLP's down projection (sixteen waves over K)
+    (5, 16384, 256),               # wide: four column tiles per block
+])
+def test_linear_small_residual_equals_torch_add(device, M, N, K):
+    """glsdm_linear_small_residual: bit-identical to torch's fp32 residual + the
+    kernel's bf16 projection, out of place and in place (out = residual)."""
+    from glsdm import _native as NT
+    from glsdm.layers.common import linear
+    g = torch.Generator().manual_seed(M + N + K)
+    lin = torch.nn.Linear(K, N).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(N, K, generator=g) / K ** 0.5).to(device))
+        lin.bias.copy_((torch.randn(N, generator=g) * 0.5).to(device))
+    x = torch.randn(M, K, generator=g).to(device=device, dtype=torch.bfloat16)
+    res = (torch.randn(M, N, generator=g) * 3).to(device)
+    with torch.no_grad():
+        proj = linear(lin, x)
+        want = res + proj
+        got = linear(lin, x, res)
+        assert got.dtype == torch.float32 and torch.equal(got, want)
+        inplace = res.clone()
+        NT.call("glsdm_linear_small_residual", NT.ptr(x), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(inplace),
+                NT.ptr(inplace), M, N, K, NT.stream(device))
+        assert torch.equal(inplace, want)
+        # a bf16 residual (or any other form) takes torch's add of the same projection
+        res16 = res.to(torch.bfloat16)
+        assert torch.equal(linear(lin, x, res16), res16 + proj)
+    # the planted slip of adding the fp32 sum before its bf16 rounding differs from torch's bits
+    assert not torch.equal(want, res + (x.float() @ lin.weight.float().T + lin.bias.float()))
+
+
 @pytest.mark.parametrize("M,widths,K,biases", [
     (64, (2048, 1024, 1024), 1024, (True, True, True)),     # a local layer's q, k, v (config 5 decode)
     (64, (1024, 16, 16), 1024, (True, True, True)),         # a global layer's v, beta, decay
