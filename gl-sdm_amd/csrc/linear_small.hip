@@ -25,6 +25,28 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
 
 constexpr int LS_MAX_ROWS = 64;
+
+// gate * bf16(relu(u)^2) rounded to bf16, for 8 bf16 pairs packed in 16 bytes
+__device__ __forceinline__ bf16x8_t relu2_gate8(uint4 u, uint4 g)
+{
+#pragma clang fp contract(off)
+    const uint32_t uw[4] = {u.x, u.y, u.z, u.w}, gw[4] = {g.x, g.y, g.z, g.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const float uf = bf16_to_f32((bf16_t)(uw[i] >> (16 * e))), gf = bf16_to_f32((bf16_t)(gw[i] >> (16 * e)));
+            const float relu = (uf > 0.0f || uf != uf) ? uf : 0.0f;   // relu keeps NaN
+            const float sq = bf16_to_f32(f32_to_bf16(relu * relu));
+            pair |= (uint32_t)f32_to_bf16(gf * sq) << (16 * e);
+        }
+        ow[i] = pair;
+    }
+    const uint4 o = {ow[0], ow[1], ow[2], ow[3]};
+    return __builtin_bit_cast(bf16x8_t, o);
+}
 constexpr int LS_MAX_GROUP = 8;
 
 // the projections of one launch (passed by value): projection i owns blocks
@@ -46,7 +68,10 @@ struct LinearGroup {
 // W waves split K (16 for deep reductions: each wave's chain of dependent k-steps
 // stays at 8 for K = 4096).  RES: the residual form, whose rounded bf16 result is
 // added in fp32 to an fp32 residual (torch's x + y for fp32 x and bf16 y).
-template <int CT, int W, bool RES>
+// RELU2: x is the MLP's fc output h [M, 2K] and the operand is formed on load,
+// a = bf16(gate * bf16(relu(u)^2)) for u = h[:, :K], gate = h[:, K:] (relu keeps
+// NaN), the roundings of the separate activation launch.
+template <int CT, int W, bool RES, bool RELU2>
 __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__restrict__ x, const LinearGroup g, int M,
                                                            int K)
 {
@@ -81,11 +106,12 @@ __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__re
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = floatx4_t{0.f, 0.f, 0.f, 0.f};
     // row li of tile rt; rows past M read row M - 1 and are never stored
+    const int64_t xstride = RELU2 ? 2 * (int64_t)K : K;
     const bf16_t *xrow[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
         const int m = rt * 16 + li < M ? rt * 16 + li : M - 1;
-        xrow[rt] = x + (int64_t)m * K + wave * kw + kq * 8;
+        xrow[rt] = x + (int64_t)m * xstride + wave * kw + kq * 8;
     }
     for (int k0 = 0; k0 < kw; k0 += 32) {
         bf16x8_t b[CT];
@@ -94,7 +120,14 @@ __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__re
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             if (rt < RT) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(xrow[rt] + k0);
+                bf16x8_t a;
+                if constexpr (RELU2) {
+                    const uint4 u = *reinterpret_cast<const uint4 *>(xrow[rt] + k0);
+                    const uint4 gt = *reinterpret_cast<const uint4 *>(xrow[rt] + K + k0);
+                    a = relu2_gate8(u, gt);
+                } else {
+                    a = *reinterpret_cast<const bf16x8_t *>(xrow[rt] + k0);
+                }
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct)
                     acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[ct], acc[rt][ct], 0, 0, 0);
@@ -135,7 +168,7 @@ namespace {
 
 // CT = 4 for wide projections (still >= 256 blocks each), 1 otherwise; W = 16 waves
 // over K for deep reductions.  W fixes the summation order; CT does not.
-template <bool RES>
+template <bool RES, bool RELU2>
 int launch_group(const bf16_t *x, LinearGroup &g, int M, int K, bool wide, hipStream_t st)
 {
     const int CT = wide ? 4 : 1;
@@ -144,11 +177,11 @@ int launch_group(const bf16_t *x, LinearGroup &g, int M, int K, bool wide, hipSt
     for (int i = g.count + 1; i <= LS_MAX_GROUP; ++i) g.first[i] = g.first[g.count];
     const dim3 grid((unsigned)g.first[g.count]);
     if (wide)
-        hipLaunchKernelGGL((linear_small_kernel<4, 4, RES>), grid, dim3(256), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<4, 4, RES, RELU2>), grid, dim3(256), 0, st, x, g, M, K);
     else if (K >= 4096 && K % (16 * 32) == 0)
-        hipLaunchKernelGGL((linear_small_kernel<1, 16, RES>), grid, dim3(1024), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<1, 16, RES, RELU2>), grid, dim3(1024), 0, st, x, g, M, K);
     else
-        hipLaunchKernelGGL((linear_small_kernel<1, 4, RES>), grid, dim3(256), 0, st, x, g, M, K);
+        hipLaunchKernelGGL((linear_small_kernel<1, 4, RES, RELU2>), grid, dim3(256), 0, st, x, g, M, K);
     return check_launch("linear_small_kernel");
 }
 
@@ -188,8 +221,8 @@ extern "C" int glsdm_linear_small(const void *x, const void *weight, const void 
     g.bias[0] = static_cast<const bf16_t *>(bias);
     g.out[0] = static_cast<bf16_t *>(out);
     g.N[0] = (int)N;
-    return launch_group<false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
-                               as_stream(stream));
+    return launch_group<false, false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
+                                      as_stream(stream));
 }
 
 extern "C" int glsdm_linear_small_residual(const void *x, const void *weight, const void *bias, const float *residual,
@@ -206,8 +239,31 @@ extern "C" int glsdm_linear_small_residual(const void *x, const void *weight, co
     g.N[0] = (int)N;
     g.residual = residual;
     g.res_out = out;
-    return launch_group<true>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
-                              as_stream(stream));
+    return launch_group<true, false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, N % 64 == 0 && N >= 16384,
+                                     as_stream(stream));
+}
+
+extern "C" int glsdm_linear_small_relu2(const void *h, const void *weight, const void *bias, const float *residual,
+                                        void *out, int64_t M, int64_t N, int64_t K, void *stream)
+{
+    int rc = check_shape(h, M, K);
+    if (rc == GLSDM_OK) rc = check_projection(weight, out, N);
+    if (rc != GLSDM_OK) return rc;
+    if (K > 0x3FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "linear_small_relu2: inner width too large");
+    LinearGroup g{};
+    g.count = 1;
+    g.w[0] = static_cast<const bf16_t *>(weight);
+    g.bias[0] = static_cast<const bf16_t *>(bias);
+    g.N[0] = (int)N;
+    const bf16_t *hh = static_cast<const bf16_t *>(h);
+    const bool wide = N % 64 == 0 && N >= 16384;
+    if (!residual) {
+        g.out[0] = static_cast<bf16_t *>(out);
+        return launch_group<false, true>(hh, g, (int)M, (int)K, wide, as_stream(stream));
+    }
+    g.residual = residual;
+    g.res_out = static_cast<float *>(out);
+    return launch_group<true, true>(hh, g, (int)M, (int)K, wide, as_stream(stream));
 }
 
 extern "C" int glsdm_linear_small_group(const void *x, int32_t count, const void *const *weights,
@@ -232,5 +288,5 @@ extern "C" int glsdm_linear_small_group(const void *x, int32_t count, const void
         blocks += N[i] / 16;
     }
     if (blocks > 0x7FFFFFFF) return fail(GLSDM_ERR_UNSUPPORTED, "linear_small_group: too many columns");
-    return launch_group<false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, wide, as_stream(stream));
+    return launch_group<false, false>(static_cast<const bf16_t *>(x), g, (int)M, (int)K, wide, as_stream(stream));
 }

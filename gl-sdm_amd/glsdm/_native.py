@@ -49,6 +49,7 @@ SIGNATURES = {
     "glsdm_relu2_gate": ([_P, _I32, _I64, _I64, _P, _P], _I32),
     "glsdm_linear_small": ([_P, _P, _P, _P, _I64, _I64, _I64, _P], _I32),
     "glsdm_linear_small_residual": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I32),
+    "glsdm_linear_small_relu2": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _P], _I32),
     "glsdm_linear_small_group": ([_P, _I32, ctypes.POINTER(_P), ctypes.POINTER(_P), ctypes.POINTER(_P),
                                   ctypes.POINTER(_I64), _I64, _I64, _P], _I32),
     "glsdm_decode_attention": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(_I64), ctypes.POINTER(_I64),

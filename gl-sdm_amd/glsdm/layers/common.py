@@ -117,10 +117,23 @@ class MLP(nn.Module):
         self.proj = nn.Linear(inner, dim)
 
     def forward(self, x, residual=None):
-        """The MLP's output, or ``residual`` plus it (one launch with the projection
-        for a decode step)."""
+        """The MLP's output, or ``residual`` plus it.  For a decode step the
+        activation and the residual add run inside the down projection's launch
+        (``glsdm_linear_small_relu2``)."""
         h = linear(self.fc, x)
         inner = h.shape[-1] // 2
+        w = self.proj.weight
+        shape = (*h.shape[:-1], w.shape[0])
+        if (_small(self.fc, x) and h.dtype == torch.bfloat16 and h.is_contiguous() and inner % 128 == 0
+                and h.data_ptr() % 16 == 0 and w.dtype == torch.bfloat16 and w.is_contiguous()
+                and w.shape[0] % 16 == 0 and w.shape[1] == inner and w.device == h.device
+                and (self.proj.bias is None or self.proj.bias.dtype == torch.bfloat16)
+                and (residual is None or (residual.dtype == torch.float32 and residual.is_contiguous()
+                                          and residual.device == h.device and tuple(residual.shape) == shape))):
+            out = torch.empty(shape, dtype=torch.bfloat16 if residual is None else torch.float32, device=h.device)
+            N.call("glsdm_linear_small_relu2", N.ptr(h), N.ptr(w), N.ptr(self.proj.bias), N.ptr(residual),
+                   N.ptr(out), h.numel() // h.shape[-1], w.shape[0], inner, N.stream(h.device))
+            return out
         if (h.is_cuda and h.dtype in (torch.float32, torch.bfloat16) and h.is_contiguous()
                 and inner % (16 // h.element_size()) == 0 and h.data_ptr() % 16 == 0
                 and not (torch.is_grad_enabled() and h.requires_grad)):

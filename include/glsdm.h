@@ -523,6 +523,21 @@ int glsdm_linear_small_residual(const void *x, const void *weight, const void *b
                                 float *out, int64_t M, int64_t N, int64_t K, void *stream);
 
 /*
+ * The MLP's down projection with its activation formed as the operand is loaded:
+ * for h [M, 2K] bf16 (the fc output; u = h[:, :K], gate = h[:, K:]) the operand is
+ * a = bf16(gate * bf16(relu(u)^2)) (glsdm_relu2_gate's roundings), then
+ *   residual NULL: out [M, N] bf16 = glsdm_linear_small of a;
+ *   otherwise:     out [M, N] fp32 = residual + float(that), as glsdm_linear_small_residual.
+ * Bit-identical to glsdm_relu2_gate followed by that call.  Requirements as
+ * glsdm_linear_small with K the inner width (h 16-byte aligned).
+ * Replaces: gate * x.relu().square() and self.proj of S/layers/common.py:26-27
+ * (and the residual add after the MLP, S/baselines/block.py:26,
+ * S/layers/global_layer.py:30) for decode-sized inputs.
+ */
+int glsdm_linear_small_relu2(const void *h, const void *weight, const void *bias, const float *residual, void *out,
+                             int64_t M, int64_t N, int64_t K, void *stream);
+
+/*
  * glsdm_linear_small for up to 8 projections of one input in one launch:
  *   outs[i] [M, N[i]] = bf16(x . weights[i]^T + biases[i]), i < count,
  * each with glsdm_linear_small's requirements and bit-identical to it (biases may

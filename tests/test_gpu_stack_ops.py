@@ -231,6 +231,48 @@ def test_linear_small_residual_equals_torch_add(device, M, N, K):
     assert not torch.equal(want, res + (x.float() @ lin.weight.float().T + lin.bias.float()))
 
 
+@pytest.mark.parametrize("M,N,K,with_residual", [
+    (64, 1024, 4096, True),        # config 5: the MLP's down projection with the block's residual
+    (64, 1024, 4096, False),
+    (17, 1024, 256, True),         # ragged rows, four waves over K
+    (3, 16384, 128, False),        # wide: four column tiles per block
+])
+def test_linear_small_relu2_equals_activation_then_projection(device, M, N, K, with_residual):
+    """glsdm_linear_small_relu2: bit-identical to glsdm_relu2_gate followed by
+    glsdm_linear_small (or its residual form), with negative, zero and positive
+    pre-activations; and the MLP routes a decode step through it."""
+    from glsdm import _native as NT
+    from glsdm.layers.common import MLP, linear, relu2_gate
+    g = torch.Generator().manual_seed(M + N + K + with_residual)
+    lin = torch.nn.Linear(K, N).to(device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_((torch.randn(N, K, generator=g) / K ** 0.5).to(device))
+        lin.bias.copy_((torch.randn(N, generator=g) * 0.5).to(device))
+    h = torch.randn(M, 2 * K, generator=g)
+    h[:, :K:7] = 0.0
+    h = h.to(device=device, dtype=torch.bfloat16)
+    res = (torch.randn(M, N, generator=g) * 3).to(device) if with_residual else None
+    with torch.no_grad():
+        want = linear(lin, relu2_gate(h), res)
+        got = torch.empty(M, N, dtype=want.dtype, device=device)
+        NT.call("glsdm_linear_small_relu2", NT.ptr(h), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(res),
+                NT.ptr(got), M, N, K, NT.stream(device))
+    assert got.dtype == (torch.float32 if with_residual else torch.bfloat16)
+    assert torch.equal(got, want)
+    # the activation's intermediate rounding matters: without it the bits differ
+    with torch.no_grad():
+        u, gate = h.float().chunk(2, -1)
+        loose = linear(lin, (gate * u.relu().square()).to(torch.bfloat16), res)
+    assert not torch.equal(loose, want)
+    if N == 1024 and K == 4096:
+        mlp = MLP(N, K).to(device=device, dtype=torch.bfloat16)
+        x = torch.randn(M, N, generator=g).to(device=device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            fc = linear(mlp.fc, x)
+            expect = linear(mlp.proj, relu2_gate(fc), res)
+            assert torch.equal(mlp(x, residual=res), expect)
+
+
 @pytest.mark.parametrize("M,widths,K,biases", [
     (64, (2048, 1024, 1024), 1024, (True, True, True)),     # a local layer's q, k, v (config 5 decode)
     (64, (1024, 16, 16), 1024, (True, True, True)),         # a global layer's v, beta, decay
