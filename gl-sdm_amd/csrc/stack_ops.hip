@@ -34,48 +34,97 @@ template <> struct RowIO<bf16_t> {
 constexpr int QK_THREADS = 256;
 constexpr int QK_MAX_DK = 256;
 
+// One row of dk = 4L elements, L lanes (lane li owns elements 2li, 2li+1 of each
+// half): RMS norm (eps = FLT_EPSILON, rounded to TX), then the rotation by the
+// position's angles in s_cos / s_sin.  The roundings of the reference's
+// F.rms_norm + rotary in TX.
+template <typename TX, int L>
+__device__ __forceinline__ void norm_rotary_row(const TX *__restrict__ src, TX *__restrict__ dst, int li,
+                                                const float *s_cos, const float *s_sin)
+{
+#pragma clang fp contract(off)
+    constexpr int dk = 4 * L, half = 2 * L;
+    const int j = 2 * li;
+    float a0 = RowIO<TX>::load(src + j), a1 = RowIO<TX>::load(src + j + 1);
+    float b0 = RowIO<TX>::load(src + half + j), b1 = RowIO<TX>::load(src + half + j + 1);
+    float ss = a0 * a0;
+    ss += a1 * a1;
+    ss += b0 * b0;
+    ss += b1 * b1;
+#pragma unroll
+    for (int off = L / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float scale = rsqrtf(ss / (float)dk + __FLT_EPSILON__);
+    a0 = RowIO<TX>::round(a0 * scale);
+    a1 = RowIO<TX>::round(a1 * scale);
+    b0 = RowIO<TX>::round(b0 * scale);
+    b1 = RowIO<TX>::round(b1 * scale);
+    const float c0 = s_cos[j], c1 = s_cos[j + 1], s0 = s_sin[j], s1 = s_sin[j + 1];
+    const float ac0 = a0 * c0, bs0 = b0 * s0, ac1 = a1 * c1, bs1 = b1 * s1;
+    const float as0 = (-a0) * s0, bc0 = b0 * c0, as1 = (-a1) * s1, bc1 = b1 * c1;
+    RowIO<TX>::store(dst + j, ac0 + bs0);
+    RowIO<TX>::store(dst + j + 1, ac1 + bs1);
+    RowIO<TX>::store(dst + half + j, as0 + bc0);
+    RowIO<TX>::store(dst + half + j + 1, as1 + bc1);
+}
+
+// cos and sin of position offset + t for the first half of the frequencies
+__device__ __forceinline__ void rotary_angles(const float *__restrict__ freq, int half, int64_t pos, float *s_cos,
+                                              float *s_sin)
+{
+    const int tid = threadIdx.x;
+    if (tid < half) {
+        const float theta = (float)pos * freq[tid];
+        s_cos[tid] = cosf(theta);
+        s_sin[tid] = sinf(theta);
+    }
+    __syncthreads();
+}
+
 template <typename TX, int L>   // L = dk / 4 lanes per row, a power of two <= 64
 __global__ __launch_bounds__(QK_THREADS) void qk_norm_rotary_kernel(const TX *__restrict__ x, int64_t row_stride,
                                                                     int64_t T, int64_t heads,
                                                                     const float *__restrict__ freq, int64_t offset,
                                                                     TX *__restrict__ out)
 {
-#pragma clang fp contract(off)
-    constexpr int dk = 4 * L, half = 2 * L, rows_per_pass = QK_THREADS / L;
+    constexpr int dk = 4 * L, rows_per_pass = QK_THREADS / L;
     __shared__ float s_cos[QK_MAX_DK / 2], s_sin[QK_MAX_DK / 2];
     const int64_t bt = blockIdx.x;                          // token b*T + t
     const int64_t t = bt % T, batch = bt / T;
-    const int tid = threadIdx.x;
-    if (tid < half) {
-        const float theta = (float)(offset + t) * freq[tid];
-        s_cos[tid] = cosf(theta);
-        s_sin[tid] = sinf(theta);
+    rotary_angles(freq, 2 * L, offset + t, s_cos, s_sin);
+    const int tid = threadIdx.x, li = tid % L;
+    for (int64_t h = tid / L; h < heads; h += rows_per_pass)      // uniform within a row's lanes
+        norm_rotary_row<TX, L>(x + (bt * heads + h) * row_stride, out + ((batch * heads + h) * T + t) * dk, li,
+                               s_cos, s_sin);
+}
+
+// A decode step's q/k preparation and KV append in one launch: per token, the
+// q rows normed and rotated into q_out [B, Hq, T, dk], the k rows normed and
+// rotated into the key buffer and the v rows copied into the value buffer, both
+// at (b, h, t) through dst strides (the buffers' slices for the new positions).
+template <typename TX, int L>
+__global__ __launch_bounds__(QK_THREADS) void decode_qkv_kernel(
+    const TX *__restrict__ q, int64_t q_stride, int64_t Hq, const TX *__restrict__ k, int64_t k_stride,
+    const TX *__restrict__ v, int64_t v_stride, int64_t Hkv, int64_t T, const float *__restrict__ freq,
+    int64_t offset, TX *__restrict__ q_out, TX *__restrict__ k_dst, TX *__restrict__ v_dst, int64_t ds0,
+    int64_t ds1, int64_t ds2)
+{
+    constexpr int dk = 4 * L, rows_per_pass = QK_THREADS / L;
+    __shared__ float s_cos[QK_MAX_DK / 2], s_sin[QK_MAX_DK / 2];
+    const int64_t bt = blockIdx.x;
+    const int64_t t = bt % T, batch = bt / T;
+    rotary_angles(freq, 2 * L, offset + t, s_cos, s_sin);
+    const int tid = threadIdx.x, li = tid % L;
+    for (int64_t h = tid / L; h < Hq + Hkv; h += rows_per_pass) {
+        if (h < Hq)
+            norm_rotary_row<TX, L>(q + (bt * Hq + h) * q_stride, q_out + ((batch * Hq + h) * T + t) * dk, li, s_cos,
+                                   s_sin);
+        else
+            norm_rotary_row<TX, L>(k + (bt * Hkv + h - Hq) * k_stride, k_dst + batch * ds0 + (h - Hq) * ds1 + t * ds2,
+                                   li, s_cos, s_sin);
     }
-    __syncthreads();
-    const int li = tid % L, j = 2 * li;
-    for (int64_t h = tid / L; h < heads; h += rows_per_pass) {     // uniform within a row's lanes
-        const TX *src = x + (bt * heads + h) * row_stride;
-        float a0 = RowIO<TX>::load(src + j), a1 = RowIO<TX>::load(src + j + 1);
-        float b0 = RowIO<TX>::load(src + half + j), b1 = RowIO<TX>::load(src + half + j + 1);
-        float ss = a0 * a0;
-        ss += a1 * a1;
-        ss += b0 * b0;
-        ss += b1 * b1;
-#pragma unroll
-        for (int off = L / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-        const float scale = rsqrtf(ss / (float)dk + __FLT_EPSILON__);
-        a0 = RowIO<TX>::round(a0 * scale);
-        a1 = RowIO<TX>::round(a1 * scale);
-        b0 = RowIO<TX>::round(b0 * scale);
-        b1 = RowIO<TX>::round(b1 * scale);
-        TX *dst = out + ((batch * heads + h) * T + t) * dk;
-        const float c0 = s_cos[j], c1 = s_cos[j + 1], s0 = s_sin[j], s1 = s_sin[j + 1];
-        const float ac0 = a0 * c0, bs0 = b0 * s0, ac1 = a1 * c1, bs1 = b1 * s1;
-        const float as0 = (-a0) * s0, bc0 = b0 * c0, as1 = (-a1) * s1, bc1 = b1 * c1;
-        RowIO<TX>::store(dst + j, ac0 + bs0);
-        RowIO<TX>::store(dst + j + 1, ac1 + bs1);
-        RowIO<TX>::store(dst + half + j, as0 + bc0);
-        RowIO<TX>::store(dst + half + j + 1, as1 + bc1);
+    for (int64_t e = tid; e < Hkv * dk; e += QK_THREADS) {
+        const int64_t h = e / dk, d = e % dk;
+        v_dst[batch * ds0 + h * ds1 + t * ds2 + d] = v[(bt * Hkv + h) * v_stride + d];
     }
 }
 
@@ -339,6 +388,57 @@ extern "C" int glsdm_gate_merge(const void *o, const int64_t *o_strides, const v
                            gate_strides[0], gate_strides[1], gate_strides[2], T, H, dk, n,
                            static_cast<bf16_t *>(out));
     return check_launch("gate_merge_kernel");
+}
+
+template <typename TX>
+static void launch_decode_qkv(const void *q, int64_t q_stride, int64_t Hq, const void *k, int64_t k_stride,
+                              const void *v, int64_t v_stride, int64_t Hkv, int64_t tokens, int64_t T, int64_t dk,
+                              const float *freq, int64_t offset, void *q_out, void *k_dst, void *v_dst,
+                              const int64_t *ds, hipStream_t st)
+{
+    const TX *qp = static_cast<const TX *>(q), *kp = static_cast<const TX *>(k), *vp = static_cast<const TX *>(v);
+    TX *qo = static_cast<TX *>(q_out), *kd = static_cast<TX *>(k_dst), *vd = static_cast<TX *>(v_dst);
+    const dim3 grid((unsigned)tokens), block(QK_THREADS);
+#define GLSDM_DQKV(LANES)                                                                                          \
+    hipLaunchKernelGGL((decode_qkv_kernel<TX, LANES>), grid, block, 0, st, qp, q_stride, Hq, kp, k_stride, vp,     \
+                       v_stride, Hkv, T, freq, offset, qo, kd, vd, ds[0], ds[1], ds[2])
+    switch (dk / 4) {
+    case 1: GLSDM_DQKV(1); break;
+    case 2: GLSDM_DQKV(2); break;
+    case 4: GLSDM_DQKV(4); break;
+    case 8: GLSDM_DQKV(8); break;
+    case 16: GLSDM_DQKV(16); break;
+    case 32: GLSDM_DQKV(32); break;
+    default: GLSDM_DQKV(64); break;
+    }
+#undef GLSDM_DQKV
+}
+
+extern "C" int glsdm_decode_qkv(const void *q, int64_t q_row_stride, int64_t q_heads, const void *k,
+                                int64_t k_row_stride, const void *v, int64_t v_row_stride, int64_t kv_heads,
+                                int32_t dtype, int64_t B, int64_t T, int64_t dk, const float *freq, int64_t offset,
+                                void *q_out, void *k_dst, void *v_dst, const int64_t *dst_strides, void *stream)
+{
+    const bool pow2 = dk >= 4 && dk <= QK_MAX_DK && (dk & (dk - 1)) == 0;
+    if (B < 0 || T < 0 || q_heads < 1 || kv_heads < 1 || !pow2 || q_row_stride < dk || k_row_stride < dk ||
+        v_row_stride < dk || offset < 0)
+        return fail(GLSDM_ERR_ARG, "decode_qkv: bad shape (dk a power of two in [4, 256], row strides >= dk)");
+    if (!dtype_ok(dtype)) return fail(GLSDM_ERR_ARG, "decode_qkv: bad dtype");
+    if (offset + T > (int64_t)1 << 24)
+        return fail(GLSDM_ERR_UNSUPPORTED, "decode_qkv: positions above 2^24 are not exact in fp32");
+    const int64_t tokens = B * T;
+    if (tokens == 0) return GLSDM_OK;
+    if (tokens > INT32_MAX) return fail(GLSDM_ERR_UNSUPPORTED, "decode_qkv: more than 2^31-1 tokens");
+    if (!q || !k || !v || !freq || !q_out || !k_dst || !v_dst || !dst_strides)
+        return fail(GLSDM_ERR_ARG, "decode_qkv: null pointer");
+    const hipStream_t st = as_stream(stream);
+    if (dtype == GLSDM_F32)
+        launch_decode_qkv<float>(q, q_row_stride, q_heads, k, k_row_stride, v, v_row_stride, kv_heads, tokens, T, dk,
+                                 freq, offset, q_out, k_dst, v_dst, dst_strides, st);
+    else
+        launch_decode_qkv<bf16_t>(q, q_row_stride, q_heads, k, k_row_stride, v, v_row_stride, kv_heads, tokens, T,
+                                  dk, freq, offset, q_out, k_dst, v_dst, dst_strides, st);
+    return check_launch("decode_qkv_kernel");
 }
 
 extern "C" int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int64_t heads, int64_t dk,

@@ -45,6 +45,8 @@ SIGNATURES = {
     "glsdm_absolute_addresses": ([_P, _I64, _I64, _I64, _I32, _I64, _P, _P], _I32),
     "glsdm_proposal_keys": ([_P, _I64, _I64, _I64, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),
     "glsdm_qk_norm_rotary": ([_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P], _I32),
+    "glsdm_decode_qkv": ([_P, _I64, _I64, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _I64, _P, _P, _P,
+                          ctypes.POINTER(_I64), _P], _I32),
     "glsdm_gate_merge": ([_P, _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "glsdm_relu2_gate": ([_P, _I32, _I64, _I64, _P, _P], _I32),
     "glsdm_linear_small": ([_P, _P, _P, _P, _I64, _I64, _I64, _P], _I32),

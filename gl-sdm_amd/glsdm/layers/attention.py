@@ -11,7 +11,9 @@ exactly the keys a full pass sees.
 
 On the GPU outside autograd, the QK normalisation and rotary run as one HIP
 kernel per projection (``glsdm_qk_norm_rotary``) that also writes the
-``[B, heads, T, dk]`` layout; under autograd and on the CPU the same
+``[B, heads, T, dk]`` layout; in a decode step one launch
+(``glsdm_decode_qkv``) does both projections' and appends the new keys and
+values to the KV window buffer.  Under autograd and on the CPU the same
 operations run as tensor ops.
 """
 import ctypes
@@ -35,6 +37,14 @@ def qk_norm_rotary(x, freq, offset):
     N.call("glsdm_qk_norm_rotary", N.ptr(x), N.dtype_code(x), B, T, heads, dk, x.stride(2), N.ptr(freq), offset,
            N.ptr(out), N.stream(x.device))
     return out
+
+
+def _token_rows(x):
+    """``x [B, T, heads, dk]`` stores row (b*T + t)*heads + h at a uniform row stride
+    with contiguous elements (the addressing of the q/k/v kernels)."""
+    B, T, H, dk = x.shape
+    return (x.stride(3) == 1 and x.stride(2) >= dk and x.stride(1) == H * x.stride(2)
+            and x.stride(0) == T * x.stride(1))
 
 
 def gate_merge(o, gate):
@@ -150,21 +160,33 @@ class Transformer(nn.Module):
         cache has one owner: two continuations of the same cache would append into
         the same buffer."""
         B, H, T, dk = k.shape
+        buf_k, buf_v, end = self._reserve(cache, previous, B, H, T, dk, k.dtype, k.device)
+        buf_k[:, :, end:end + T].copy_(k)
+        buf_v[:, :, end:end + T].copy_(v)
+        return self._finish(cache, buf_k, buf_v, end, previous, T, offset)
+
+    @staticmethod
+    def _reserve(cache, previous, B, H, T, dk, dtype, device):
+        """The cache's KV window buffers with room for T more rows after its
+        ``previous`` rows, which end at the returned position (a fresh buffer, the
+        kept rows copied in, when the room has run out)."""
         buf_k, buf_v, end = cache.get("kbuf"), cache.get("vbuf"), cache.get("end", 0)
         tail = cache.get("k")
         in_buffer = (buf_k is not None and tail is not None and tail.shape[2] == previous and previous <= end
                      and (previous == 0 or tail.data_ptr() == buf_k[:, :, end - previous:end].data_ptr()))
-        if not in_buffer or end + T > buf_k.shape[2] or buf_k.dtype != k.dtype or buf_k.device != k.device:
+        if not in_buffer or end + T > buf_k.shape[2] or buf_k.dtype != dtype or buf_k.device != device:
             room = max(512, T)
             cap = previous + T + room
-            buf_k = torch.empty((B, H, cap, dk), dtype=k.dtype, device=k.device)
-            buf_v = torch.empty((B, H, cap, dk), dtype=v.dtype, device=v.device)
+            buf_k = torch.empty((B, H, cap, dk), dtype=dtype, device=device)
+            buf_v = torch.empty((B, H, cap, dk), dtype=dtype, device=device)
             if previous:
                 buf_k[:, :, :previous].copy_(cache["k"])
                 buf_v[:, :, :previous].copy_(cache["v"])
             end = previous
-        buf_k[:, :, end:end + T].copy_(k)
-        buf_v[:, :, end:end + T].copy_(v)
+        return buf_k, buf_v, end
+
+    def _finish(self, cache, buf_k, buf_v, end, previous, T, offset):
+        """Record T rows appended at ``end``; the visible keys and values as views."""
         start, end = end - previous, end + T
         n = previous + T
         keep = n if self.window is None else min(self.window - 1, n)
@@ -183,13 +205,29 @@ class Transformer(nn.Module):
         offset = 0 if cache is None else cache.get("tokens", previous)
         fused = (x.is_cuda and dk in (4, 8, 16, 32, 64, 128, 256) and x.dtype in (torch.float32, torch.bfloat16) and offset + T <= 1 << 24
                  and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad)))
+        appended = False
         if fused:
             freq = self.angular_freq.float().contiguous()
-            q, k = qk_norm_rotary(q, freq, offset), qk_norm_rotary(k, freq, offset)
+            vt = v.transpose(1, 2)                     # [B, T, kv_heads, dk]
+            if (cache is not None and T <= APPEND_MAX_TOKENS and self.append_in_place and q.dtype == k.dtype == v.dtype
+                    and _token_rows(q) and _token_rows(k) and _token_rows(vt)):
+                # decode: q/k norm and rotary and the KV append in one launch
+                buf_k, buf_v, end = self._reserve(cache, previous, B, self.num_kv_heads, T, dk, k.dtype, k.device)
+                q_out = torch.empty((B, self.num_heads, T, dk), dtype=q.dtype, device=q.device)
+                dst = buf_k[:, :, end:end + T]
+                N.call("glsdm_decode_qkv", N.ptr(q), q.stride(2), self.num_heads, N.ptr(k), k.stride(2), N.ptr(vt),
+                       vt.stride(2), self.num_kv_heads, N.dtype_code(q), B, T, dk, N.ptr(freq), offset, N.ptr(q_out),
+                       N.ptr(dst), N.ptr(buf_v[:, :, end:end + T]), (ctypes.c_int64 * 3)(*dst.stride()[:3]),
+                       N.stream(q.device))
+                q = q_out
+                k, v = self._finish(cache, buf_k, buf_v, end, previous, T, offset)
+                appended = True
+            else:
+                q, k = qk_norm_rotary(q, freq, offset), qk_norm_rotary(k, freq, offset)
         else:
             q = self.rotary(F.rms_norm(q, (dk,)), offset).transpose(1, 2)
             k = self.rotary(F.rms_norm(k, (dk,)), offset).transpose(1, 2)
-        if cache is not None:
+        if cache is not None and not appended:
             if (T > APPEND_MAX_TOKENS or not self.append_in_place
                     or (torch.is_grad_enabled() and (k.requires_grad or v.requires_grad))):
                 # prefill chunks, functional caches and autograd: concatenation (attention

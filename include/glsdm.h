@@ -474,6 +474,23 @@ int glsdm_qk_norm_rotary(const void *x, int32_t dtype, int64_t B, int64_t T, int
                          int64_t row_stride, const float *freq, int64_t offset, void *out, void *stream);
 
 /*
+ * A local layer's decode-step preparation in one launch: glsdm_qk_norm_rotary of
+ * the q rows (q + ((b*T + t)*q_heads + h)*q_row_stride) into q_out [B, q_heads,
+ * T, dk] contiguous, of the k rows (same addressing with kv_heads, k_row_stride)
+ * into k_dst, and a copy of the v rows (v_row_stride) into v_dst, where element
+ * d of (b, h, t) of k_dst / v_dst is at b*s[0] + h*s[1] + t*s[2] + d for
+ * s = dst_strides (the KV window buffers' slices for the new positions).
+ * Bit-identical to two glsdm_qk_norm_rotary calls and the two copies; limits
+ * as glsdm_qk_norm_rotary.
+ * Replaces: S/layers/attention.py:38-42,51-52 (q/k norm and rotary) and the
+ * cache concatenation of S/layers/attention.py:55 for a decode step.
+ */
+int glsdm_decode_qkv(const void *q, int64_t q_row_stride, int64_t q_heads, const void *k, int64_t k_row_stride,
+                     const void *v, int64_t v_row_stride, int64_t kv_heads, int32_t dtype, int64_t B, int64_t T,
+                     int64_t dk, const float *freq, int64_t offset, void *q_out, void *k_dst, void *v_dst,
+                     const int64_t *dst_strides, void *stream);
+
+/*
  * The gated attention output: out[b, t, h*dk + i] = o[b, h, t, i] *
  * sigmoid(gate[b, t, h, i]) (sigmoid in fp32 rounded to dtype, then the
  * product rounded to dtype), o [B, H, T, dk] and gate [B, T, H, dk] read

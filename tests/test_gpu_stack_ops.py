@@ -231,6 +231,43 @@ def test_linear_small_residual_equals_torch_add(device, M, N, K):
     assert not torch.equal(want, res + (x.float() @ lin.weight.float().T + lin.bias.float()))
 
 
+@pytest.mark.parametrize("B,T,Hq,Hkv,dk,dtype", [
+    (64, 1, 16, 16, 64, torch.bfloat16),     # config 5: one token per stream
+    (3, 5, 4, 2, 128, torch.bfloat16),      # several tokens, grouped KV heads
+    (2, 2, 8, 8, 32, torch.float32),
+])
+def test_decode_qkv_equals_norm_rotary_and_copies(device, B, T, Hq, Hkv, dk, dtype):
+    """glsdm_decode_qkv: q_out and the new buffer rows bit-identical to
+    glsdm_qk_norm_rotary of q and k and a copy of v; the buffer rows around the
+    new positions untouched."""
+    import ctypes
+    from glsdm import _native as NT
+    from glsdm.layers.attention import qk_norm_rotary
+    g = torch.Generator().manual_seed(B * 100 + T + dk)
+    qg = torch.randn(B, T, Hq, 2 * dk, generator=g).to(device=device, dtype=dtype)
+    q = qg[..., :dk]                                              # the query half of [query | gate]
+    k = torch.randn(B, T, Hkv, dk, generator=g).to(device=device, dtype=dtype)
+    v = torch.randn(B, T, Hkv, dk, generator=g).to(device=device, dtype=dtype)
+    rising = torch.pow(torch.tensor(1 / 1024), torch.linspace(0, 1, dk // 4))
+    freq = torch.cat((rising, torch.zeros_like(rising))).to(device)
+    offset, end, cap = 700, 9, 9 + T + 6
+    buf_k = torch.randn(B, Hkv, cap, dk, generator=g).to(device=device, dtype=dtype)
+    buf_v = torch.randn(B, Hkv, cap, dk, generator=g).to(device=device, dtype=dtype)
+    want_k, want_v = buf_k.clone(), buf_v.clone()
+    with torch.no_grad():
+        want_q = qk_norm_rotary(q, freq, offset)
+        want_k[:, :, end:end + T] = qk_norm_rotary(k, freq, offset)
+        want_v[:, :, end:end + T] = v.transpose(1, 2)
+        q_out = torch.empty(B, Hq, T, dk, dtype=dtype, device=device)
+        dst = buf_k[:, :, end:end + T]
+        NT.call("glsdm_decode_qkv", NT.ptr(q), q.stride(2), Hq, NT.ptr(k), k.stride(2), NT.ptr(v), v.stride(2), Hkv,
+                NT.dtype_code(q), B, T, dk, NT.ptr(freq), offset, NT.ptr(q_out), NT.ptr(dst),
+                NT.ptr(buf_v[:, :, end:end + T]), (ctypes.c_int64 * 3)(*dst.stride()[:3]), NT.stream(device))
+    assert torch.equal(q_out, want_q)
+    assert torch.equal(buf_k, want_k)
+    assert torch.equal(buf_v, want_v)
+
+
 @pytest.mark.parametrize("M,N,K,with_residual", [
     (64, 1024, 4096, True),        # config 5: the MLP's down projection with the block's residual
     (64, 1024, 4096, False),
