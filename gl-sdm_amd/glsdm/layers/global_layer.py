@@ -43,7 +43,10 @@ class GlobalLayer(nn.Module):
         router = self.attn
         dtype = router.q.weight.dtype
         scores = linear(router.q, self.norm1.cast(x, dtype)).view(B, T, router.heads, -1)
-        readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical)
+        # outside autograd the read rounds its fp32 sums to the projection dtype itself
+        grad = torch.is_grad_enabled() and (x.requires_grad or snapshot.values.requires_grad)
+        readings, _, _ = routing.routed_read(self, snapshot.values, scores, router.num_reads, physical,
+                                             out_dtype=torch.float32 if grad else dtype)
         x = linear(router.proj, router.read_norm(readings.to(dtype)).flatten(-2), x)
         x = self.mlp(self.norm2.cast(x, dtype), residual=x)
         return x, regulariser(x, self.reg_mode), zero(x)

@@ -36,12 +36,13 @@ def _host_copy(values):
     return _HOST[1]
 
 
-def _routed_read(block, memory, scores, width, physical=None):
+def _routed_read(block, memory, scores, width, physical=None, out_dtype=torch.float32):
     del physical
     device = scores.device
     # the reference routes the fp32 widening of the projection (S/layers/global_layer.py:26,42)
+    # and reads in fp32; a bf16 out_dtype is its later .to(dtype) of the readings
     out, index, weights = torch_oracle.routed_read(_host_copy(memory), scores.cpu().float(), width, block.attn.tie)
-    return out.to(device), index.to(device), weights.to(device)
+    return out.to(device=device, dtype=out_dtype), index.to(device), weights.to(device)
 
 
 def _layer_proposal(snapshot, index, weights, prediction, target, beta, log_decay, offset, layer_idx, chunk_size,
@@ -134,14 +135,17 @@ class Shadow:
         native_read, native_propose, native_commit = routing.routed_read, global_layer.layer_proposal, stack.commit
         native_log = global_layer.log_proposal
 
-        def read(block, memory, scores, width, physical=None):
-            out, index, weights = native_read(block, memory, scores, width, physical)
+        def read(block, memory, scores, width, physical=None, out_dtype=torch.float32):
+            out, index, weights = native_read(block, memory, scores, width, physical, out_dtype=out_dtype)
             host = self._host(memory)
             r_out, r_idx, r_w = torch_oracle.routed_read(host, scores.cpu().float(), width, block.attn.tie)
             where = f"read {self.reads}"
             assert torch.equal(index.cpu(), r_idx), f"{where}: routes differ from the oracle"
             torch.testing.assert_close(weights.cpu(), r_w, atol=2e-7, rtol=2e-6, msg=lambda m: f"{where}: {m}")
-            torch.testing.assert_close(out.cpu(), r_out, **self.read_tol, msg=lambda m: f"{where}: {m}")
+            # readings rounded to bf16 by the read: the oracle's rounded alike, within one bf16 step
+            tol = self.read_tol if out.dtype == torch.float32 else dict(atol=self.read_tol["atol"], rtol=2 ** -7)
+            torch.testing.assert_close(out.cpu().float(), r_out.to(out.dtype).float(), **tol,
+                                       msg=lambda m: f"{where}: {m}")
             self.reads += 1
             return out, index, weights
 
@@ -217,8 +221,8 @@ class RouteLog:
         layer_of = {id(b): i for i, b in enumerate(model.blocks)}
         native = routing.routed_read
 
-        def read(block, memory, scores, width, physical=None):
-            out = native(block, memory, scores, width, physical)
+        def read(block, memory, scores, width, physical=None, out_dtype=torch.float32):
+            out = native(block, memory, scores, width, physical, out_dtype=out_dtype)
             kind = 1 if sys._getframe(1).f_code.co_name == "propose" else 0
             layer = layer_of[id(block)]
             start = self._seen.get((layer, kind), 0)

@@ -62,6 +62,10 @@ def test_read_bf16_output(device):
     out = hip.snapshot_read(mem.to(device), idx.to(device), w.to(device), out_dtype=torch.bfloat16)
     ref = c_oracle.read(mem, idx, w)
     torch.testing.assert_close(out.cpu().float(), ref, atol=1e-4, rtol=2e-2)
+    # the fp32 sums rounded once: the bits of an fp32 read followed by .to(bfloat16)
+    # (the stack's global layers read straight into bf16 on this)
+    wide = hip.snapshot_read(mem.to(device), idx.to(device), w.to(device), out_dtype=torch.float32)
+    assert torch.equal(out, wide.to(torch.bfloat16))
 
 
 def test_read_out_of_range_slots_contribute_nothing(device):
