@@ -14,7 +14,9 @@
 // p_j * v_j with lane d owning output dimension d (each value row is one
 // coalesced 128-byte read); the four partial results are merged in wave order.
 // Keys and values are read through (request, head, key) strides, so the cache's
-// window views need no copy.
+// window views need no copy.  With a gate, the output row is multiplied by
+// bf16(sigmoid(gate)) and rounded again (the local layer's output gate,
+// S/layers/attention.py:77, with the roundings of its bf16 tensor ops).
 #include "glsdm_internal.h"
 
 namespace glsdm {
@@ -27,7 +29,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const bf16_t *__r
                                                                const bf16_t *__restrict__ v, bf16_t *__restrict__ out,
                                                                int64_t H, int L, int64_t ksb, int64_t ksh,
                                                                int64_t ksl, int64_t vsb, int64_t vsh, int64_t vsl,
-                                                               float scale)
+                                                               float scale, const bf16_t *__restrict__ gate,
+                                                               int64_t gsb, int64_t gsh)
 {
 #pragma clang fp contract(off)
     __shared__ float s_p[4][DA_MAX_KEYS / 4];
@@ -36,6 +39,8 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const bf16_t *__r
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t bh = blockIdx.x, b = bh / H, h = bh % H;
     const bf16_t *kb = k + b * ksb + h * ksh, *vb = v + b * vsb + h * vsh;
+    // the gate element of output dimension threadIdx.x, loaded before the key loop
+    const float gval = gate && threadIdx.x < DK ? bf16_to_f32(gate[b * gsb + h * gsh + threadIdx.x]) : 0.0f;
     // the query row in fp32 registers (every lane holds all of it)
     float qf[DK];
 #pragma unroll
@@ -121,7 +126,13 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const bf16_t *__r
             num = num + f * s_acc[w][d];
             den = den + f * s_l[w];
         }
-        out[bh * DK + d] = f32_to_bf16(num / den);
+        if (gate) {
+            const float a = bf16_to_f32(f32_to_bf16(num / den));
+            const float sig = bf16_to_f32(f32_to_bf16(1.0f / (1.0f + expf(-gval))));
+            out[bh * DK + d] = f32_to_bf16(a * sig);
+        } else {
+            out[bh * DK + d] = f32_to_bf16(num / den);
+        }
     }
 }
 
@@ -129,26 +140,50 @@ __global__ __launch_bounds__(256) void decode_attention_kernel(const bf16_t *__r
 
 using namespace glsdm;
 
-extern "C" int glsdm_decode_attention(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H,
-                                      int64_t L, int64_t dk, const int64_t *k_strides, const int64_t *v_strides,
-                                      float scale, void *stream)
+namespace {
+
+int decode_attention(const void *q, const void *k, const void *v, const void *gate, void *out, int64_t B, int64_t H,
+                     int64_t L, int64_t dk, const int64_t *k_strides, const int64_t *v_strides,
+                     const int64_t *gate_strides, float scale, void *stream)
 {
     if (B < 1 || H < 1 || L < 1 || dk < 1) return fail(GLSDM_ERR_ARG, "decode_attention: bad shape");
     if (L > DA_MAX_KEYS || (dk != 64 && dk != 128))
         return fail(GLSDM_ERR_UNSUPPORTED, "decode_attention: at most 1024 keys and dk 64 or 128");
-    if (!q || !k || !v || !out || !k_strides || !v_strides) return fail(GLSDM_ERR_ARG, "decode_attention: null pointer");
+    if (!q || !k || !v || !out || !k_strides || !v_strides || (gate && !gate_strides))
+        return fail(GLSDM_ERR_ARG, "decode_attention: null pointer");
     if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15) != 0 || k_strides[2] % 8 != 0 ||
         k_strides[0] % 8 != 0 || k_strides[1] % 8 != 0)
         return fail(GLSDM_ERR_UNSUPPORTED, "decode_attention: query and key rows must be 16-byte aligned");
     const bf16_t *qq = static_cast<const bf16_t *>(q), *kk = static_cast<const bf16_t *>(k),
-                 *vv = static_cast<const bf16_t *>(v);
+                 *vv = static_cast<const bf16_t *>(v), *gg = static_cast<const bf16_t *>(gate);
     bf16_t *oo = static_cast<bf16_t *>(out);
+    const int64_t gsb = gate ? gate_strides[0] : 0, gsh = gate ? gate_strides[1] : 0;
     const dim3 grid((unsigned)(B * H)), block(256);
     if (dk == 64)
         hipLaunchKernelGGL((decode_attention_kernel<64>), grid, block, 0, as_stream(stream), qq, kk, vv, oo, H, (int)L,
-                           k_strides[0], k_strides[1], k_strides[2], v_strides[0], v_strides[1], v_strides[2], scale);
+                           k_strides[0], k_strides[1], k_strides[2], v_strides[0], v_strides[1], v_strides[2], scale,
+                           gg, gsb, gsh);
     else
         hipLaunchKernelGGL((decode_attention_kernel<128>), grid, block, 0, as_stream(stream), qq, kk, vv, oo, H, (int)L,
-                           k_strides[0], k_strides[1], k_strides[2], v_strides[0], v_strides[1], v_strides[2], scale);
+                           k_strides[0], k_strides[1], k_strides[2], v_strides[0], v_strides[1], v_strides[2], scale,
+                           gg, gsb, gsh);
     return check_launch("decode_attention_kernel");
+}
+
+}  // namespace
+
+extern "C" int glsdm_decode_attention(const void *q, const void *k, const void *v, void *out, int64_t B, int64_t H,
+                                      int64_t L, int64_t dk, const int64_t *k_strides, const int64_t *v_strides,
+                                      float scale, void *stream)
+{
+    return decode_attention(q, k, v, nullptr, out, B, H, L, dk, k_strides, v_strides, nullptr, scale, stream);
+}
+
+extern "C" int glsdm_decode_attention_gated(const void *q, const void *k, const void *v, const void *gate, void *out,
+                                            int64_t B, int64_t H, int64_t L, int64_t dk, const int64_t *k_strides,
+                                            const int64_t *v_strides, const int64_t *gate_strides, float scale,
+                                            void *stream)
+{
+    if (!gate) return fail(GLSDM_ERR_ARG, "decode_attention_gated: null gate");
+    return decode_attention(q, k, v, gate, out, B, H, L, dk, k_strides, v_strides, gate_strides, scale, stream);
 }

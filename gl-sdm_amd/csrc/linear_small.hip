@@ -113,26 +113,44 @@ __global__ __launch_bounds__(64 * W) void linear_small_kernel(const bf16_t *__re
         const int m = rt * 16 + li < M ? rt * 16 + li : M - 1;
         xrow[rt] = x + (int64_t)m * xstride + wave * kw + kq * 8;
     }
-    for (int k0 = 0; k0 < kw; k0 += 32) {
-        bf16x8_t b[CT];
+    // Every k-step loads its weight fragments and all four row tiles (rows past M
+    // read row M - 1, a valid address, and their results are never stored) with no
+    // branch between the loads, and two k-steps are loaded before either's MFMAs,
+    // so up to 2 * (CT + 4) loads are in flight before the first wait.  The MFMAs
+    // of each (row tile, column tile) still run in k order.
+    auto load = [&](int k0, bf16x8_t (&b)[CT], bf16x8_t (&a)[4]) {
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) b[ct] = *reinterpret_cast<const bf16x8_t *>(wrow[ct] + k0);
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-            if (rt < RT) {
-                bf16x8_t a;
-                if constexpr (RELU2) {
-                    const uint4 u = *reinterpret_cast<const uint4 *>(xrow[rt] + k0);
-                    const uint4 gt = *reinterpret_cast<const uint4 *>(xrow[rt] + K + k0);
-                    a = relu2_gate8(u, gt);
-                } else {
-                    a = *reinterpret_cast<const bf16x8_t *>(xrow[rt] + k0);
-                }
-#pragma unroll
-                for (int ct = 0; ct < CT; ++ct)
-                    acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[ct], acc[rt][ct], 0, 0, 0);
+            if constexpr (RELU2) {
+                const uint4 u = *reinterpret_cast<const uint4 *>(xrow[rt] + k0);
+                const uint4 gt = *reinterpret_cast<const uint4 *>(xrow[rt] + K + k0);
+                a[rt] = relu2_gate8(u, gt);
+            } else {
+                a[rt] = *reinterpret_cast<const bf16x8_t *>(xrow[rt] + k0);
             }
         }
+    };
+    auto multiply = [&](const bf16x8_t (&b)[CT], const bf16x8_t (&a)[4]) {
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rt], b[ct], acc[rt][ct], 0, 0, 0);
+    };
+    int k0 = 0;
+    for (; k0 + 64 <= kw; k0 += 64) {
+        bf16x8_t b0[CT], a0[4], b1[CT], a1[4];
+        load(k0, b0, a0);
+        load(k0 + 32, b1, a1);
+        multiply(b0, a0);
+        multiply(b1, a1);
+    }
+    if (k0 < kw) {
+        bf16x8_t b0[CT], a0[4];
+        load(k0, b0, a0);
+        multiply(b0, a0);
     }
     // acc[rt][ct][i]: row rt*16 + 4*kq + i, column n0 + 16 ct + li
 #pragma unroll

@@ -56,6 +56,8 @@ SIGNATURES = {
                                   ctypes.POINTER(_I64), _I64, _I64, _P], _I32),
     "glsdm_decode_attention": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
                                 ctypes.c_float, _P], _I32),
+    "glsdm_decode_attention_gated": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(_I64),
+                                      ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.c_float, _P], _I32),
     "glsdm_rms_norm_cast": ([_P, _I32, _P, _I32, _I64, _I64, ctypes.c_float, _P, _I32, _P], _I32),
     "glsdm_write_gates": ([_P, _P, _I32, _I64, _P, _P, _P], _I32),
     "glsdm_gather_rows": ([_P, _I32, _I64, _I64, _P, _I64, _P, _P], _I32),

@@ -63,20 +63,30 @@ _MASKS = {}
 APPEND_MAX_TOKENS = 16    # calls of at most this many tokens (decode) append to the KV window in place
 
 
-def decode_attention(q, k, v):
+def decode_attention(q, k, v, gate=None):
     """``F.scaled_dot_product_attention(q, k, v)`` for one query row per (request,
     head), ``q [B, H, 1, dk]`` contiguous bf16, ``k``/``v [B, H, L, dk]`` strided
     views with unit last stride, no mask (``glsdm_decode_attention``: fp32 scores,
-    softmax and sums, rounded once; within rounding of the library's kernel)."""
+    softmax and sums, rounded once; within rounding of the library's kernel).
+    With ``gate [B, 1, H, dk]`` (unit last stride) the result is
+    ``gate_merge(attention, gate)`` as ``[B, 1, H*dk]``, in the same launch."""
     B, H, _, dk = q.shape
     L = k.shape[2]
     if k.stride(-1) != 1 or v.stride(-1) != 1:
         raise ValueError("decode_attention needs unit-stride key and value rows")
-    out = torch.empty_like(q)
     ks = (ctypes.c_int64 * 3)(*k.stride()[:3])
     vs = (ctypes.c_int64 * 3)(*v.stride()[:3])
-    N.call("glsdm_decode_attention", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(out), B, H, L, dk, ks, vs,
-           ctypes.c_float(dk ** -0.5), N.stream(q.device))
+    if gate is None:
+        out = torch.empty_like(q)
+        N.call("glsdm_decode_attention", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(out), B, H, L, dk, ks, vs,
+               ctypes.c_float(dk ** -0.5), N.stream(q.device))
+        return out
+    if gate.shape != (B, 1, H, dk) or gate.stride(-1) != 1 or gate.dtype != q.dtype:
+        raise ValueError("decode_attention needs a gate [B, 1, H, dk] of the query dtype with unit-stride rows")
+    out = torch.empty((B, 1, H * dk), dtype=q.dtype, device=q.device)
+    gs = (ctypes.c_int64 * 2)(gate.stride(0), gate.stride(2))
+    N.call("glsdm_decode_attention_gated", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gate), N.ptr(out), B, H, L, dk, ks,
+           vs, gs, ctypes.c_float(dk ** -0.5), N.stream(q.device))
     return out
 
 
@@ -252,7 +262,10 @@ class Transformer(nn.Module):
                 and (self.window is None or previous < self.window) and q.is_contiguous()
                 and not (torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad))):
             # one token per request with every cached key inside its window (the mask is
-            # all zeros): one HIP launch instead of the library's attention
+            # all zeros): one HIP launch instead of the library's attention, the output
+            # gate applied in it
+            if gate.stride(-1) == 1 and gate.dtype == q.dtype:
+                return linear(self.proj, decode_attention(q, k, v, gate), residual)
             out = decode_attention(q, k, v)
         else:
             mask = None

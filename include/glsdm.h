@@ -581,6 +581,19 @@ int glsdm_decode_attention(const void *q, const void *k, const void *v, void *ou
                            int64_t dk, const int64_t *k_strides, const int64_t *v_strides, float scale, void *stream);
 
 /*
+ * glsdm_decode_attention with the local layer's output gate applied to each
+ * output row: out[b, h, d] = bf16(bf16(attention) * bf16(sigmoid(g))) for
+ * g = gate[b*gate_strides[0] + h*gate_strides[1] + d] (bf16; sigmoid = 1/(1 +
+ * exp(-g)) in fp32), written as [B, H*dk] -- the input of proj for one token.
+ * Bit-identical to glsdm_decode_attention followed by glsdm_gate_merge.
+ * Replaces: S/layers/attention.py:76-77 (attention and the gate before proj)
+ * for a decode step.
+ */
+int glsdm_decode_attention_gated(const void *q, const void *k, const void *v, const void *gate, void *out,
+                                 int64_t B, int64_t H, int64_t L, int64_t dk, const int64_t *k_strides,
+                                 const int64_t *v_strides, const int64_t *gate_strides, float scale, void *stream);
+
+/*
  * RMSNorm then a cast: per row of x [rows, dim] (x_dtype), r =
  * rsqrt(mean(x^2) + eps), y = (x*r)*w in fp32 rounded to x_dtype (w [dim] of
  * w_dtype, rounded to x_dtype first), y written as out_dtype to out [rows, dim].

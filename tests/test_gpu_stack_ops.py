@@ -231,6 +231,23 @@ def test_linear_small_residual_equals_torch_add(device, M, N, K):
     assert not torch.equal(want, res + (x.float() @ lin.weight.float().T + lin.bias.float()))
 
 
+@pytest.mark.parametrize("B,H,L,dk", [(64, 16, 512, 64), (2, 4, 77, 128), (3, 2, 1, 64)])
+def test_decode_attention_gated_equals_attention_then_gate_merge(device, B, H, L, dk):
+    """glsdm_decode_attention_gated: bit-identical to glsdm_decode_attention then
+    glsdm_gate_merge, with the gate read from the [query | gate] projection layout."""
+    from glsdm.layers.attention import decode_attention, gate_merge
+    g = torch.Generator().manual_seed(B + H + L + dk)
+    q = torch.randn(B, H, 1, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    k = torch.randn(B, H, L, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    v = torch.randn(B, H, L, dk, generator=g).to(device=device, dtype=torch.bfloat16)
+    qg = (torch.randn(B, 1, H, 2 * dk, generator=g) * 3).to(device=device, dtype=torch.bfloat16)
+    gate = qg[..., dk:]
+    with torch.no_grad():
+        want = gate_merge(decode_attention(q, k, v), gate)
+        got = decode_attention(q, k, v, gate)
+    assert got.shape == (B, 1, H * dk) and torch.equal(got, want)
+
+
 @pytest.mark.parametrize("B,T,Hq,Hkv,dk,dtype", [
     (64, 1, 16, 16, 64, torch.bfloat16),     # config 5: one token per stream
     (3, 5, 4, 2, 128, torch.bfloat16),      # several tokens, grouped KV heads
