@@ -145,9 +145,15 @@ def lib():
     return _lib
 
 
+_fns = {}
+
+
 def call(name, *args):
     """Invoke an entry point and turn a non-zero status into an exception."""
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != OK:
         msg = lib().glsdm_last_error().decode()
         if rc in (ERR_ARG, ERR_UNSUPPORTED, ERR_WORKSPACE):

@@ -41,12 +41,25 @@ def linear(layer, x, residual=None):
 
 
 def _small(layer, x):
-    w = layer.weight
+    """Whether ``glsdm_linear_small`` takes ``layer(x)``: the input checks run per
+    call, the weight's (dtype, width, layout, bias dtype, device) are kept on the
+    module with the storage, dtype and device they were made for (a decode step
+    asks this over a hundred times)."""
+    if torch.is_grad_enabled() or x.dtype != torch.bfloat16 or not x.is_cuda:
+        return False
     K = x.shape[-1]
-    return (not torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
-            and x.numel() <= 64 * K and w.shape[0] % 16 == 0 and K % 128 == 0 and x.is_contiguous()
-            and x.data_ptr() % 16 == 0 and w.is_contiguous() and w.device == x.device
-            and (layer.bias is None or layer.bias.dtype == torch.bfloat16))
+    if K % 128 or x.numel() > 64 * K or not x.is_contiguous() or x.data_ptr() % 16:
+        return False
+    params = layer._parameters
+    w, b = params["weight"], params.get("bias")
+    key = (w.data_ptr(), w.dtype, w.device, None if b is None else (b.data_ptr(), b.dtype))
+    memo = layer.__dict__.get("_glsdm_small")
+    if memo is None or memo[0] != key:
+        ok = (w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[0] % 16 == 0 and w.is_contiguous()
+              and (b is None or b.dtype == torch.bfloat16))
+        memo = (key, ok)
+        layer.__dict__["_glsdm_small"] = memo
+    return memo[1] and w.shape[1] == K and w.device == x.device
 
 
 def linear_group(layers, x):
