@@ -85,7 +85,7 @@ def forward(model, inputs, cache=None):
                and any(isinstance(b, GlobalLayer) for b in model.blocks)
                and _all_logged(cache))
     outputs = []
-    reg, align = inputs.new_zeros(()), inputs.new_zeros(())
+    reg = align = None          # sums of the blocks' terms that are not the shared zeros
     position = 0
     while position < T:
         offset = cache.tokens % C
@@ -103,7 +103,9 @@ def forward(model, inputs, cache=None):
             else:
                 x, r, a = block(x, cache.local.setdefault(i, {}))
             if r is not zero(r) or a is not zero(a):     # the baseline's are the shared zeros: nothing to add
-                reg, align = reg + r * (length / T), align + a
+                term = r * (length / T)
+                reg = term if reg is None else reg + term
+                align = a if align is None else align + a
         cache.tokens += length
         if cache.tokens % C == 0 and writes:
             cache.view = commit(snapshot, merge(snapshot, proposals), donate=in_place)
@@ -116,4 +118,8 @@ def forward(model, inputs, cache=None):
             cache._all_logged = (cache.pending, logged)
         outputs.append(x)
         position += length
-    return torch.cat(outputs, 1), reg / layers, align / layers
+    # one chunk (every decode step) needs no concatenation; with only zero terms the
+    # regularisers are the shared read-only zero (no fill or division launches)
+    hidden = outputs[0] if len(outputs) == 1 else torch.cat(outputs, 1)
+    z = zero(inputs)
+    return hidden, z if reg is None else reg / layers, z if align is None else align / layers
