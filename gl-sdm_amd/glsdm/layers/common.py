@@ -70,17 +70,28 @@ def linear_group(layers, x):
     if not 1 < len(layers) <= 8 or not all(_small(l, x) for l in layers):
         return [linear(l, x) for l in layers]
     K, M = x.shape[-1], x.numel() // x.shape[-1]
-    widths = [l.weight.shape[0] for l in layers]
-    flat = torch.empty(M * sum(widths), dtype=torch.bfloat16, device=x.device)
-    outs, at = [], 0
-    for n in widths:
-        outs.append(flat[at:at + M * n].view(*x.shape[:-1], n))
-        at += M * n
+    # the weight and bias pointer arrays and the widths are kept on the first
+    # module with the modules and storages they were made for
+    key = tuple((id(l), l._parameters["weight"].data_ptr(),
+                 0 if l._parameters.get("bias") is None else l._parameters["bias"].data_ptr()) for l in layers)
+    memo = layers[0].__dict__.get("_glsdm_group")
     count = len(layers)
     P = N.ctypes.c_void_p
-    N.call("glsdm_linear_small_group", N.ptr(x), count, (P * count)(*(l.weight.data_ptr() for l in layers)),
-           (P * count)(*(0 if l.bias is None else l.bias.data_ptr() for l in layers)),
-           (P * count)(*(o.data_ptr() for o in outs)), (N.ctypes.c_int64 * count)(*widths), M, K, N.stream(x.device))
+    if memo is None or memo[0] != key:
+        widths = [l._parameters["weight"].shape[0] for l in layers]
+        memo = (key, widths, sum(widths), (P * count)(*(k[1] for k in key)), (P * count)(*(k[2] for k in key)),
+                (N.ctypes.c_int64 * count)(*widths))
+        layers[0].__dict__["_glsdm_group"] = memo
+    _, widths, total, weights, biases, width_arr = memo
+    flat = torch.empty(M * total, dtype=torch.bfloat16, device=x.device)
+    base, lead = flat.data_ptr(), x.shape[:-1]
+    outs, ptrs, at = [], [], 0
+    for n in widths:
+        outs.append(flat[at:at + M * n].view(*lead, n))
+        ptrs.append(base + 2 * at)
+        at += M * n
+    N.call("glsdm_linear_small_group", N.ptr(x), count, weights, biases, (P * count)(*ptrs), width_arr, M, K,
+           N.stream(x.device))
     return outs
 
 

@@ -363,6 +363,17 @@ def test_linear_small_group_equals_separate_calls(device, M, widths, K, biases):
             if lin.bias is not None:
                 ref = ref + lin.bias.double().cpu()
             torch.testing.assert_close(out.double().cpu(), ref, rtol=8e-3, atol=1e-3 * ref.abs().max().item())
+    # a second call reuses the group's kept pointer arrays; a weight given new storage
+    # (new values) is seen
+    with torch.no_grad():
+        layers[-1].weight.data = layers[-1].weight.data * 2
+        again = linear_group(layers, x)
+        for lin, out, before in zip(layers, again, outs):
+            alone = torch.empty(M, lin.out_features, dtype=torch.bfloat16, device=device)
+            NT.call("glsdm_linear_small", NT.ptr(x), NT.ptr(lin.weight), NT.ptr(lin.bias), NT.ptr(alone), M,
+                    lin.out_features, K, NT.stream(device))
+            assert torch.equal(out, alone)
+        assert torch.equal(again[0], outs[0]) and not torch.equal(again[-1], outs[-1])
     # an ineligible member (a width not a multiple of 16) sends every projection to torch
     odd = torch.nn.Linear(K, 24).to(device=device, dtype=torch.bfloat16)
     with torch.no_grad():
