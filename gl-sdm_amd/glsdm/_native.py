@@ -162,15 +162,18 @@ def call(name, *args):
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    """A tensor's device address for a ``void *`` argument (None for None): a plain
+    int, which ctypes converts for the declared pointer type without building a
+    c_void_p object (a decode step passes several hundred of them)."""
+    return t.data_ptr() if t is not None else None
 
 
 def stream(device):
-    """The current HIP stream of ``device`` as a ctypes pointer (torch's raw-stream
-    query: a decode step makes over a hundred native calls, and the Stream-object
-    path costs several microseconds of host time each)."""
+    """The current HIP stream of ``device`` as an address for a ``void *`` argument
+    (torch's raw-stream query: a decode step makes over a hundred native calls, and
+    the Stream-object path costs several microseconds of host time each)."""
     index = device.index if device.index is not None else torch.cuda.current_device()
-    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def dtype_code(t):
