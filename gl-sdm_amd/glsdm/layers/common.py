@@ -117,14 +117,17 @@ class RMSNorm(nn.Module):
     def cast(self, x, dtype):
         """``self(x).to(dtype)``; on the GPU outside autograd one HIP launch
         (``glsdm_rms_norm_cast``) instead of the norm and the cast."""
-        w = self.weight
-        kinds = (torch.float32, torch.bfloat16)
-        if (x.is_cuda and x.dtype in kinds and dtype in kinds and w.dtype in kinds and w.is_contiguous()
+        w = self._parameters["weight"]
+        codes = N.DTYPES
+        xc, oc, wc = codes.get(x.dtype), codes.get(dtype), codes.get(w.dtype)
+        if (x.is_cuda and xc is not None and oc is not None and wc is not None and w.is_contiguous()
                 and not (torch.is_grad_enabled() and (x.requires_grad or w.requires_grad))):
-            x = x.contiguous()
+            if not x.is_contiguous():
+                x = x.contiguous()
             out = torch.empty(x.shape, dtype=dtype, device=x.device)
-            N.call("glsdm_rms_norm_cast", N.ptr(x), N.dtype_code(x), N.ptr(w), N.dtype_code(w),
-                   x.numel() // x.shape[-1], x.shape[-1], 1e-6, N.ptr(out), N.dtype_code(out), N.stream(x.device))
+            dim = x.shape[-1]
+            N.call("glsdm_rms_norm_cast", x.data_ptr(), xc, w.data_ptr(), wc, x.numel() // dim, dim, 1e-6,
+                   out.data_ptr(), oc, N.stream(x.device))
             return out
         return self(x).to(dtype)
 
