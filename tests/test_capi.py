@@ -163,3 +163,46 @@ def test_stack_ops_reject_bad_arguments_before_launch():
     assert append(1, 4096, 0, 1) == N.ERR_UNSUPPORTED      # D above 2048
     assert append(1, 64, 0, 7) == N.ERR_ARG                # gate dtype
     assert append(0, 64, 0, 1) == N.OK                     # empty
+
+
+def test_decode_entry_points_reject_bad_arguments_before_launch():
+    """The decode-step entry points (projections, q/k/v preparation, attention)
+    check counts, shapes and alignment on the host; nothing is launched on these."""
+    one, odd = ctypes.c_void_p(16), ctypes.c_void_p(18)
+    lin = lambda name, x, M, Nn, K: _rc(name, x, one, None, one, M, Nn, K, None)
+    for name in ("glsdm_linear_small",):
+        assert lin(name, one, 65, 16, 128) == N.ERR_UNSUPPORTED      # more than 64 rows
+        assert lin(name, one, 4, 24, 128) == N.ERR_UNSUPPORTED       # width not a multiple of 16
+        assert lin(name, one, 4, 16, 96) == N.ERR_UNSUPPORTED        # depth not a multiple of 128
+        assert lin(name, odd, 4, 16, 128) == N.ERR_UNSUPPORTED       # x not 16-byte aligned
+        assert lin(name, one, 0, 16, 128) == N.ERR_ARG               # no rows
+    res = lambda M, Nn, K, r: _rc("glsdm_linear_small_residual", one, one, None, r, one, M, Nn, K, None)
+    assert res(4, 16, 128, None) == N.ERR_ARG                       # residual missing
+    assert res(4, 24, 128, one) == N.ERR_UNSUPPORTED
+    relu = lambda h, M, Nn, K: _rc("glsdm_linear_small_relu2", h, one, None, None, one, M, Nn, K, None)
+    assert relu(one, 4, 16, 100) == N.ERR_UNSUPPORTED               # inner width not a multiple of 128
+    assert relu(odd, 4, 16, 128) == N.ERR_UNSUPPORTED
+    P = ctypes.c_void_p
+    ptrs = (P * 9)(*([16] * 9))
+    widths = (ctypes.c_int64 * 9)(*([16] * 9))
+    group = lambda count, w: _rc("glsdm_linear_small_group", one, count, ptrs, None, ptrs, w, 4, 128, None)
+    assert group(0, widths) == N.ERR_ARG                             # no projection
+    assert group(9, widths) == N.ERR_ARG                             # more than 8
+    assert group(2, (ctypes.c_int64 * 2)(16, 40)) == N.ERR_UNSUPPORTED   # a width not a multiple of 16
+    # decode_qkv(q, q_stride, q_heads, k, k_stride, v, v_stride, kv_heads, dtype, B, T, dk, freq, offset,
+    #            q_out, k_dst, v_dst, dst_strides, stream)
+    strides = (ctypes.c_int64 * 3)(1024, 64, 64)
+    qkv = lambda dk, ks, offset, dtype: _rc("glsdm_decode_qkv", one, 2 * dk, 4, one, ks, one, dk, 4, dtype, 2, 1,
+                                            dk, one, offset, one, one, one, strides, None)
+    assert qkv(48, 48, 0, 1) == N.ERR_ARG                            # dk not a power of two
+    assert qkv(64, 32, 0, 1) == N.ERR_ARG                            # key row stride below dk
+    assert qkv(64, 64, 1 << 24, 1) == N.ERR_UNSUPPORTED              # positions not exact in fp32
+    assert qkv(64, 64, 0, 4) == N.ERR_ARG                            # dtype
+    kv = (ctypes.c_int64 * 3)(64 * 512, 512 * 64, 64)
+    gs = (ctypes.c_int64 * 2)(1024, 128)
+    att = lambda L, dk, gate: _rc("glsdm_decode_attention_gated", one, one, one, gate, one, 2, 4, L, dk, kv, kv, gs,
+                                  ctypes.c_float(0.125), None)
+    assert att(1025, 64, one) == N.ERR_UNSUPPORTED                   # more than 1024 keys
+    assert att(16, 96, one) == N.ERR_UNSUPPORTED                     # dk other than 64 / 128
+    assert att(16, 64, None) == N.ERR_ARG                            # gate missing
+
