@@ -3,11 +3,18 @@
 activation ``gate * relu(u)^2`` is one HIP launch (``glsdm_relu2_gate``, the
 same roundings as the tensor ops), and the stack's projections of decode-sized
 inputs run ``glsdm_linear_small`` (``linear``)."""
+import weakref
+
 import torch
 from torch import nn
 import torch.nn.functional as F
 
 from .. import _native as N
+
+# per-module host-side memos of the decode projections (kept off the modules, so
+# copying or pickling a model never meets the ctypes arrays)
+_SMALL = weakref.WeakKeyDictionary()
+_GROUP = weakref.WeakKeyDictionary()
 
 
 def linear(layer, x, residual=None):
@@ -42,9 +49,9 @@ def linear(layer, x, residual=None):
 
 def _small(layer, x):
     """Whether ``glsdm_linear_small`` takes ``layer(x)``: the input checks run per
-    call, the weight's (dtype, width, layout, bias dtype, device) are kept on the
-    module with the storage, dtype and device they were made for (a decode step
-    asks this over a hundred times)."""
+    call, the weight's (dtype, width, layout, bias dtype) are kept per module with
+    the storage, dtype and device they were made for (a decode step asks this over
+    a hundred times)."""
     if torch.is_grad_enabled() or x.dtype != torch.bfloat16 or not x.is_cuda:
         return False
     K = x.shape[-1]
@@ -53,12 +60,12 @@ def _small(layer, x):
     params = layer._parameters
     w, b = params["weight"], params.get("bias")
     key = (w.data_ptr(), w.dtype, w.device, None if b is None else (b.data_ptr(), b.dtype))
-    memo = layer.__dict__.get("_glsdm_small")
+    memo = _SMALL.get(layer)
     if memo is None or memo[0] != key:
         ok = (w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[0] % 16 == 0 and w.is_contiguous()
               and (b is None or b.dtype == torch.bfloat16))
         memo = (key, ok)
-        layer.__dict__["_glsdm_small"] = memo
+        _SMALL[layer] = memo
     return memo[1] and w.shape[1] == K and w.device == x.device
 
 
@@ -70,18 +77,18 @@ def linear_group(layers, x):
     if not 1 < len(layers) <= 8 or not all(_small(l, x) for l in layers):
         return [linear(l, x) for l in layers]
     K, M = x.shape[-1], x.numel() // x.shape[-1]
-    # the weight and bias pointer arrays and the widths are kept on the first
-    # module with the modules and storages they were made for
+    # the weight and bias pointer arrays and the widths are kept per first module
+    # with the modules and storages they were made for
     key = tuple((id(l), l._parameters["weight"].data_ptr(),
                  0 if l._parameters.get("bias") is None else l._parameters["bias"].data_ptr()) for l in layers)
-    memo = layers[0].__dict__.get("_glsdm_group")
+    memo = _GROUP.get(layers[0])
     count = len(layers)
     P = N.ctypes.c_void_p
     if memo is None or memo[0] != key:
         widths = [l._parameters["weight"].shape[0] for l in layers]
         memo = (key, widths, sum(widths), (P * count)(*(k[1] for k in key)), (P * count)(*(k[2] for k in key)),
                 (N.ctypes.c_int64 * count)(*widths))
-        layers[0].__dict__["_glsdm_group"] = memo
+        _GROUP[layers[0]] = memo
     _, widths, total, weights, biases, width_arr = memo
     flat = torch.empty(M * total, dtype=torch.bfloat16, device=x.device)
     base, lead = flat.data_ptr(), x.shape[:-1]

@@ -374,6 +374,14 @@ def test_linear_small_group_equals_separate_calls(device, M, widths, K, biases):
                     lin.out_features, K, NT.stream(device))
             assert torch.equal(out, alone)
         assert torch.equal(again[0], outs[0]) and not torch.equal(again[-1], outs[-1])
+    # the host-side memos stay off the modules: a used group still copies and pickles,
+    # and the copy (its own storages) computes the same
+    import copy
+    import pickle
+    clone = copy.deepcopy(layers)
+    pickle.dumps(layers)
+    with torch.no_grad():
+        assert all(torch.equal(a, b) for a, b in zip(linear_group(clone, x), linear_group(layers, x)))
     # an ineligible member (a width not a multiple of 16) sends every projection to torch
     odd = torch.nn.Linear(K, 24).to(device=device, dtype=torch.bfloat16)
     with torch.no_grad():
